@@ -1,0 +1,475 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Each oracle function is checked against (a) the reference's own golden
+vectors (tests/native/conformance/fixtures, copied as data under
+tests/golden/wgsl) at the reference harness's tolerances, and (b) what the
+mathematics fixes: closed forms in float64, exhaustive sweeps and brute
+force, chosen so that a dropped term, a swapped nibble or a wrong index
+fails at least one check. The fixtures were produced by the WGSL kernels,
+so where WGSL and WASM semantics differ (S6 rope rounding, S10 top-k slot
+order, exact exp vs the polynomial) the comparison says so.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from parity_util import dequant_rows, f16, fp16_ieee, fp16_ulp_diff, rel_err_max, rel_err_norm
+from textsift_amd import synth
+from textsift_amd.config import PF_CONFIG
+
+
+# ---------------------------------------------------------------- conversions
+
+def test_fp16_known_answers():
+    # zig/math.zig:177-191
+    for v in (0.0, 1.0, -1.0, 2.5, -3.25, 1024.0):
+        assert oracle.lib().pfo_fp16_to_f32(oracle.lib().pfo_f32_to_fp16(v)) == v
+    for bits, v in ((0x0000, 0.0), (0x3C00, 1.0), (0xBC00, -1.0), (0x5000, 32.0)):
+        assert oracle.lib().pfo_fp16_to_f32(bits) == v
+
+
+def test_fp16_widen_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = oracle.fp16_to_f32(bits).astype(np.float64)
+    exp = bits & 0x7C00
+    mant = (bits & 0x3FF).astype(np.float64)
+    sign = np.where(bits & 0x8000, -1.0, 1.0)
+    normal = (exp != 0) & (exp != 0x7C00)
+    assert np.array_equal(got[normal], f16(bits)[normal])
+    # S1: zero stays zero, subnormal m -> 2^-15 (1 + m/1024), inf/NaN -> 2^16 (1 + m/1024)
+    zero = (bits & 0x7FFF) == 0
+    assert np.all(got[zero] == 0.0)
+    sub = (exp == 0) & ~zero
+    assert np.array_equal(got[sub], (sign * 2.0 ** -15 * (1 + mant / 1024))[sub])
+    top = exp == 0x7C00
+    assert np.array_equal(got[top], (sign * 2.0 ** 16 * (1 + mant / 1024))[top])
+
+
+def test_fp16_narrow_normals_match_ieee_rne():
+    x = np.concatenate([
+        synth.normal(1, 200000, 0, 30.0),
+        synth.uniform(2, 200000, -65000, 65000),
+        synth.uniform(3, 100000, 6.2e-5, 1e-3),
+        # exact ties between two fp16 neighbours (RNE must go to even)
+        (np.arange(1024, 2048) + 0.5) * 2.0 ** -10,
+    ]).astype(np.float32)
+    x = x[np.abs(x) >= 2.0 ** -14]
+    got = oracle.f32_to_fp16(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_fp16_narrow_subnormal_round_half_up():
+    # S2: subnormal results round half UP (zig/math.zig:68-73), not to even.
+    lsb = 2.0 ** -24
+    for k in range(0, 1023, 7):
+        half = np.float32((k + 0.5) * lsb)
+        assert oracle.lib().pfo_f32_to_fp16(float(half)) == k + 1
+        below = np.nextafter(half, np.float32(0))
+        assert oracle.lib().pfo_f32_to_fp16(float(below)) == k
+    assert oracle.lib().pfo_f32_to_fp16(1e-9) == 0
+    assert oracle.lib().pfo_f32_to_fp16(70000.0) == 0x7C00
+    assert oracle.lib().pfo_f32_to_fp16(float("inf")) == 0x7C00
+
+
+def test_exp_approx_closed_form():
+    # zig/wasm_exports.zig:812-838: 2^floor(y) * P5(frac). The polynomial's
+    # coefficients sum to 1.99944746 at frac=1, so its true accuracy is
+    # ~2.8e-4 relative (the source comment's 3e-7 does not hold); the GPU
+    # path reproduces the polynomial, not exp.
+    x = np.linspace(-87.0, 0.0, 401, dtype=np.float32)
+    got = np.array([oracle.lib().pfo_exp_approx(float(v)) for v in x])
+    y = x * np.float32(1.44269504088896340736)          # f32 product, as the kernel
+    fl = np.floor(y).astype(np.float64)
+    fr = (y - np.floor(y)).astype(np.float64)            # exact in f32
+    poly = 0.0
+    for c in (0.001333355, 0.009679494, 0.055053319, 0.240226522, 0.693154774, 1.000000012):
+        poly = poly * fr + c
+    ref = poly * 2.0 ** fl
+    assert np.max(np.abs(got - ref) / ref) < 1e-6
+    true = np.exp(x.astype(np.float64))
+    assert 2.0e-4 < np.max(np.abs(got - true) / true) < 3.0e-4
+    # S8: a -inf logit contributes exactly 0
+    assert oracle.lib().pfo_exp_approx(float("-inf")) == 0.0
+
+
+# ---------------------------------------------------------------- gather / dequant
+
+def test_embed_fixture_bit_exact(fixture):
+    fx = fixture("embed_lookup_int4")
+    T, V, D, _ = fx.uniform_u32
+    got = oracle.embed_lookup(fx.input("embed_int4"), fx.input("embed_scales", np.uint16), fx.input("embed_zp"),
+                              fx.input("ids", np.int32), V, D)
+    assert np.array_equal(got.ravel(), fx.expected(np.uint16))
+
+
+def test_embed_closed_form_and_oob():
+    V, D, T = 300, 640, 257
+    w = synth.qweight(11, V, D, zp=None, bias_sigma=None)
+    ids = synth.token_ids(12, T, V)
+    ids[[0, 5, 77]] = [-1, V, V + 1000]
+    got = oracle.embed_lookup(w["int4"], w["scales"], w["zp"], ids, V, D)
+    deq = dequant_rows(w["int4"], w["scales"], w["zp"], V, D)
+    valid = (ids >= 0) & (ids < V)
+    ref = np.zeros((T, D), np.float64)
+    ref[valid] = deq[ids[valid]]
+    # one RNE rounding of an exact product (<= 15 significant bits)
+    assert np.array_equal(got, fp16_ieee(ref))
+    assert np.all(got[~valid] == 0)
+
+
+# ---------------------------------------------------------------- MatMulNBits
+
+def test_matmul_fp16_fixture(fixture):
+    fx = fixture("matmul_int4_fp16_f16")
+    T, N, K, _ = fx.uniform_u32
+    got = oracle.matmul(fx.input("x", np.uint16), fx.input("w_int4"), fx.input("w_scales", np.uint16),
+                        fx.input("w_zp"), fx.input("bias", np.uint16), N, K, x_f32=False, out_f32=False)
+    ulp = fp16_ulp_diff(got.ravel(), fx.expected(np.uint16))
+    assert ulp.max() <= 1.0
+
+
+def test_matmul_f32_fixture(fixture):
+    fx = fixture("matmul_int4_f32_f32")
+    T, N, K, _ = fx.uniform_u32
+    got = oracle.matmul(fx.input("x", np.float32), fx.input("w_int4"), fx.input("w_scales", np.uint16),
+                        fx.input("w_zp"), fx.input("bias", np.uint16), N, K, x_f32=True, out_f32=True)
+    exp = fx.expected(np.float32)
+    # The fixture's WGSL kernel is one thread per (t, n) and was dispatched
+    # with 1 workgroup of 64 threads, so only the first 64 outputs were
+    # written; the rest of expected.bin is the zero-initialised buffer.
+    n = fx.meta["dispatch"][0] * 64
+    assert np.all(exp[n:] == 0)
+    assert np.max(np.abs(got.ravel()[:n] - exp[:n]) / np.maximum(np.abs(exp[:n]), 1e-6)) < 1e-5
+
+
+@pytest.mark.parametrize("T", [1, 7, 8, 13, 64])
+@pytest.mark.parametrize("zp", [8, None])
+def test_matmul_closed_form(T, zp):
+    N, K = 96, 640
+    w = synth.qweight(21 + T, N, K, zp=zp)
+    x = synth.normal(22 + T, T * K).astype(np.float32).reshape(T, K)
+    deq = dequant_rows(w["int4"], w["scales"], w["zp"], N, K)
+    ref = x.astype(np.float64) @ deq.T + f16(w["bias"])
+    # f32 summation error bound: K * 2^-24 * sum|x_k w_k| (cancellation-safe)
+    bound = K * 2.0 ** -24 * (np.abs(x.astype(np.float64)) @ np.abs(deq).T + np.abs(f16(w["bias"])))
+    got32 = oracle.matmul(x, w["int4"], w["scales"], w["zp"], w["bias"], N, K, x_f32=True, out_f32=True)
+    assert rel_err_norm(got32, ref) < 2e-6
+    assert np.all(np.abs(got32 - ref) <= bound)
+    got16 = oracle.matmul(x, w["int4"], w["scales"], w["zp"], w["bias"], N, K, x_f32=True, out_f32=False)
+    assert np.mean(fp16_ulp_diff(got16, fp16_ieee(ref)) <= 0.5) > 0.99
+    assert np.array_equal(got16, oracle.f32_to_fp16(got32))
+
+
+def test_matmul_tail_vs_main_path_order():
+    # S4: the T tail (T mod 8 rows) sums in a different order than the TR=8
+    # path, so row r of a T=9 call equals row r of a T=8 call for r < 8 but the
+    # 9th row equals a T=1 call on that row.
+    N, K = 32, 640
+    w = synth.qweight(31, N, K)
+    x = synth.normal(32, 9 * K).astype(np.float32).reshape(9, K)
+    a = oracle.matmul(x, w["int4"], w["scales"], w["zp"], w["bias"], N, K, True, True)
+    b = oracle.matmul(x[:8], w["int4"], w["scales"], w["zp"], w["bias"], N, K, True, True)
+    c = oracle.matmul(x[8:], w["int4"], w["scales"], w["zp"], w["bias"], N, K, True, True)
+    assert np.array_equal(a[:8], b) and np.array_equal(a[8:], c)
+
+
+# ---------------------------------------------------------------- norms
+
+def test_rms_norm_fixture(fixture):
+    fx = fixture("rms_norm")
+    T, D = fx.uniform_u32[:2]
+    eps = float(fx.uniform_f32[2])
+    got = oracle.rms_norm(fx.input("x", np.uint16), fx.input("gamma", np.uint16), T, D, eps)
+    assert fp16_ulp_diff(got.ravel(), fx.expected(np.uint16)).max() <= 1.0
+
+
+def test_add_rmsnorm_fixture(fixture):
+    fx = fixture("add_rmsnorm_fp16_to_f32")
+    T, D = fx.uniform_u32[:2]
+    eps = float(fx.uniform_f32[2])
+    s, n = oracle.add_rmsnorm_f32(fx.input("a", np.uint16), fx.input("b", np.uint16), fx.input("gamma", np.uint16),
+                                  T, D, eps)
+    exp = fx.expected(np.float32)
+    assert np.max(np.abs(n.ravel() - exp) / np.maximum(np.abs(exp), 1e-6)) < 1e-5
+
+
+def test_rms_norm_f32_closed_form():
+    T, D = 33, 640
+    x = synth.to_fp16_bits(synth.normal(41, T * D, 0, 3)).reshape(T, D)
+    g = synth.to_fp16_bits(synth.normal(42, D, 1, 0.1))
+    got = oracle.rms_norm_f32(x, g, T, D, 1e-5)
+    xv = f16(x)
+    ref = xv / np.sqrt(np.mean(xv * xv, axis=1, keepdims=True) + 1e-5) * f16(g)
+    assert rel_err_max(got, ref) < 1e-6
+
+
+# ---------------------------------------------------------------- routing
+
+def test_router_topk_fixture_scores(fixture):
+    # The WGSL kernel emits slot order (S10); compare sorted per row.
+    fx = fixture("router_topk")
+    T, E, K, _ = fx.uniform_u32
+    logits = fx.input("logits", np.float32).reshape(T, E)
+    idx, w = oracle.router_select(logits, T, E, K)
+    exp = np.sort(fx.expected(np.float32).reshape(T, K), axis=1)
+    assert np.max(np.abs(np.sort(w, axis=1) - exp)) < 1e-7
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_topk_brute_force_with_ties(seed):
+    T, E, K = 257, 128, 4
+    x = np.round(synth.normal(50 + seed, T * E, 0, 2), 1).astype(np.float32).reshape(T, E)  # many ties
+    idx, val = oracle.topk(x, T, E, K)
+    # sorted by value descending, ties -> lower index first
+    order = np.lexsort((np.arange(E)[None, :].repeat(T, 0), -x), axis=1)[:, :K]
+    assert np.array_equal(idx, order)
+    assert np.array_equal(val, np.take_along_axis(x, order, 1))
+
+
+def test_router_weights_closed_form():
+    T, E, K = 64, 128, 4
+    x = synth.normal(60, T * E, 0, 1.5).astype(np.float32).reshape(T, E)
+    idx, w = oracle.router_select(x, T, E, K)
+    top = np.take_along_axis(x, idx, 1).astype(np.float64)
+    sm = np.exp(top - top.max(1, keepdims=True))
+    sm /= sm.sum(1, keepdims=True)
+    assert np.max(np.abs(w - sm / K)) < 1e-7
+
+
+# ---------------------------------------------------------------- SwiGLU / MoE
+
+def test_swiglu_fixture(fixture):
+    fx = fixture("swiglu_clamp")
+    T, D = fx.uniform_u32[:2]
+    got = oracle.swiglu(fx.input("gate_up", np.float32), T, D)
+    exp = fx.expected(np.float32)
+    # WGSL uses exact exp, WASM the polynomial (<= 2.8e-4 relative in exp);
+    # the reference harness allows 1e-2 relative for f32 outputs.
+    assert np.max(np.abs(got.ravel() - exp) / np.maximum(np.abs(exp), 1e-6)) < 5e-4
+
+
+def test_swiglu_closed_form():
+    T, D = 16, 640
+    gu = synth.normal(70, T * 2 * D, 0, 5).reshape(T, 2 * D).astype(np.float32)
+    got = oracle.swiglu(gu, T, D)
+    g = np.minimum(gu[:, 0::2].astype(np.float64), 7)
+    u = np.clip(gu[:, 1::2].astype(np.float64), -7, 7)
+    ref = (u + 1) * g / (1 + np.exp(-1.702 * g))
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-3)) < 5e-4
+
+
+def _qmoe_expected_gate_up(fx):
+    T, K, N, D = fx.uniform_u32[:4]
+    x = fx.input("x", np.float32).reshape(T, D)
+    ridx = fx.input("routing_idx", np.int32).reshape(T, K)
+    E = fx.input("w_int4").size // (N * D // 2)
+    out = np.empty((T * K, N), np.float32)
+    wi, ws, wz, wb = fx.input("w_int4"), fx.input("w_scales", np.uint16), fx.input("w_zp"), fx.input("bias", np.uint16)
+    nb = D // 32
+    for t in range(T):
+        for k in range(K):
+            e = ridx[t, k]
+            sl = slice(e * N * D // 2, (e + 1) * N * D // 2)
+            out[t * K + k] = oracle.matmul(x[t:t + 1], wi[sl], ws[e * N * nb:(e + 1) * N * nb],
+                                           wz[e * N * ((nb + 1) // 2):(e + 1) * N * ((nb + 1) // 2)],
+                                           wb[e * N:(e + 1) * N], N, D, True, True)[0]
+    return out
+
+
+def test_qmoe_gate_up_fixture(fixture):
+    fx = fixture("qmoe_gate_up")
+    got = _qmoe_expected_gate_up(fx)
+    exp = fx.expected(np.float32)
+    assert rel_err_max(got.ravel(), exp) < 1e-6
+
+
+def test_qmoe_down_scatter_fixture(fixture):
+    fx = fixture("qmoe_down_scatter")
+    T, K, N, D = fx.uniform_u32[:4]
+    glu = fx.input("glu", np.float32).reshape(T * K, D)
+    ridx = fx.input("routing_idx", np.int32).reshape(T, K)
+    rw = fx.input("routing_scores", np.float32).reshape(T, K)
+    acc = fx.raw("_output_initial.bin", np.float32).reshape(T, N).copy()
+    wi, ws, wz, wb = fx.input("w_int4"), fx.input("w_scales", np.uint16), fx.input("w_zp"), fx.input("bias", np.uint16)
+    nb = D // 32
+    for t in range(T):
+        for k in range(K):
+            e = ridx[t, k]
+            y = oracle.matmul(glu[t * K + k:t * K + k + 1], wi[e * N * D // 2:(e + 1) * N * D // 2],
+                              ws[e * N * nb:(e + 1) * N * nb],
+                              wz[e * N * ((nb + 1) // 2):(e + 1) * N * ((nb + 1) // 2)], wb[e * N:(e + 1) * N],
+                              N, D, True, True)[0]
+            acc[t] = acc[t] + rw[t, k] * y
+    assert rel_err_max(acc.ravel(), fx.expected(np.float32)) < 1e-6
+
+
+def test_expert_dispatch_closed_form():
+    """expertDispatch vs a float64 restatement of the MoE FFN."""
+    cfg = PF_CONFIG
+    E, T, D, F = 8, 37, cfg.hidden_size, cfg.intermediate_size
+    w = {}
+    for k, v in synth.qweight(80, 2 * F, D, lead=(E,)).items():
+        w[f"layers.0.experts.gate_up.{k}"] = v
+    for k, v in synth.qweight(81, D, F, lead=(E,)).items():
+        w[f"layers.0.experts.down.{k}"] = v
+    # the dispatch wrapper builds a full layer struct; fill unused slots
+    for name in ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.o_proj", "router"):
+        for k, v in synth.qweight(82, 64, 64).items():
+            w[f"layers.0.{name}.{k}"] = v
+    w["layers.0.input_layernorm"] = w["layers.0.post_attention_layernorm"] = np.zeros(D, np.uint16)
+    w["layers.0.attn.sinks"] = np.zeros(14, np.float32)
+    h = synth.normal(83, T * D).astype(np.float32).reshape(T, D)
+    ridx = np.stack([np.random.default_rng(t).choice(E, 4, replace=False) for t in range(T)]).astype(np.int32)
+    rw = synth.uniform(84, T * 4, 0.01, 0.4).astype(np.float32).reshape(T, 4)
+    got1 = oracle.expert_dispatch(cfg, w, 0, h, ridx, rw, n_slices=1)
+    got3 = oracle.expert_dispatch(cfg, w, 0, h, ridx, rw, n_slices=3)
+    gu = [dequant_rows(w["layers.0.experts.gate_up.int4"][e], w["layers.0.experts.gate_up.scales"][e],
+                       w["layers.0.experts.gate_up.zp"][e], 2 * F, D) for e in range(E)]
+    dn = [dequant_rows(w["layers.0.experts.down.int4"][e], w["layers.0.experts.down.scales"][e],
+                       w["layers.0.experts.down.zp"][e], D, F) for e in range(E)]
+    ref = np.zeros((T, D))
+    for t in range(T):
+        for k in range(4):
+            e = ridx[t, k]
+            a = h[t].astype(np.float64) @ gu[e].T + f16(w["layers.0.experts.gate_up.bias"][e])
+            g, u = np.minimum(a[0::2], 7), np.clip(a[1::2], -7, 7)
+            glu = (u + 1) * g / (1 + np.exp(-1.702 * g))
+            ref[t] += rw[t, k] * (glu @ dn[e].T + f16(w["layers.0.experts.down.bias"][e]))
+    ref *= 4
+    # the polynomial sigmoid (<= 2.8e-4 in exp) dominates the difference
+    assert rel_err_norm(f16(got1), ref) < 3e-4
+    # worker slicing only regroups the f32 GEMM rows (S4)
+    assert rel_err_norm(f16(got3), f16(got1)) < 1e-5
+
+
+# ---------------------------------------------------------------- attention / rope
+
+def test_banded_attention_fixture(fixture):
+    fx = fixture("banded_attention")
+    T, Hq, Hkv, hd, W, use_mask = fx.uniform_u32[:6]
+    mask = fx.input("mask").astype(np.uint8)[:T] if use_mask else None
+    got = oracle.banded_attention(fx.input("q", np.uint16), fx.input("k", np.uint16), fx.input("v", np.uint16),
+                                  fx.input("sinks", np.float32), mask, T, Hq, Hkv, hd, W)
+    # WGSL uses exact exp, WASM the polynomial (S9): normwise, not per-ulp.
+    assert rel_err_norm(f16(got.ravel()), f16(fx.expected(np.uint16))) < 5e-4
+    assert rel_err_max(f16(got.ravel()), f16(fx.expected(np.uint16))) < 1e-3
+
+
+def exp_poly64(x):
+    """float64 evaluation of expApproxNonPositiveF32x4's formula (f32 y)."""
+    y = np.maximum(np.asarray(x, np.float32), np.float32(-88.0)) * np.float32(1.44269504088896340736)
+    fl = np.floor(y)
+    fr = (y - fl).astype(np.float64)
+    poly = np.zeros_like(fr)
+    for c in (0.001333355, 0.009679494, 0.055053319, 0.240226522, 0.693154774, 1.000000012):
+        poly = poly * fr + c
+    return np.where(fl < -126, 0.0, poly * 2.0 ** fl.astype(np.float64))
+
+
+def attention_ref64(q, k, v, sinks, mask, T, Hq, Hkv, hd, W, scale=1.0, exp=np.exp):
+    """float64 banded GQA softmax with sinks (zig/wasm_exports.zig:1197-1227)."""
+    qf = f16(q).reshape(T, Hq, hd)
+    kf = f16(k).reshape(T, Hkv, hd)
+    vf = f16(v).reshape(T, Hkv, hd)
+    out = np.zeros((T, Hq, hd))
+    g = Hq // Hkv
+    for t in range(T):
+        ws, we = max(0, t - W), min(T, t + W + 1)
+        for h in range(Hq):
+            s = kf[ws:we, h // g] @ qf[t, h] * scale
+            if mask is not None:
+                s = np.where(mask[ws:we] != 0, s, -np.inf)
+            m = max(s.max(), sinks[h])
+            e = exp(s - m)
+            den = e.sum() + exp(np.float64(sinks[h]) - m)
+            out[t, h] = (e / den) @ vf[ws:we, h // g]
+    return out.reshape(T, Hq * hd)
+
+
+@pytest.mark.parametrize("T,W,masked", [(40, 4, False), (300, 128, False), (64, 16, True)])
+def test_banded_attention_closed_form(T, W, masked):
+    Hq, Hkv, hd = 14, 2, 64
+    q = synth.to_fp16_bits(synth.normal(90 + T, T * Hq * hd, 0, 0.4))
+    k = synth.to_fp16_bits(synth.normal(91 + T, T * Hkv * hd, 0, 0.4))
+    v = synth.to_fp16_bits(synth.normal(92 + T, T * Hkv * hd))
+    sinks = synth.normal(93, Hq).astype(np.float32)
+    mask = (synth.uniform(94, T) > 0.3).astype(np.uint8) if masked else None
+    got = oracle.banded_attention(q, k, v, sinks, mask, T, Hq, Hkv, hd, W)
+    # with the kernel's polynomial exp the structure is pinned to ~1 ulp ...
+    ref_poly = attention_ref64(q, k, v, sinks.astype(np.float64), mask, T, Hq, Hkv, hd, W, exp=exp_poly64)
+    assert np.mean(fp16_ulp_diff(got, fp16_ieee(ref_poly)) <= 1.0) > 0.99
+    assert rel_err_norm(f16(got), ref_poly) < 3e-4   # fp16 output rounding
+    # ... and against true exp it stays within the polynomial's error
+    ref = attention_ref64(q, k, v, sinks.astype(np.float64), mask, T, Hq, Hkv, hd, W)
+    assert rel_err_norm(f16(got), ref) < 6e-4
+
+
+def test_rope_fixture(fixture):
+    # WGSL rounds the final sub/add once in f16; WASM rounds an f32 result
+    # (S6). Reference tolerance for this kernel is 32 ulp.
+    fx = fixture("rope_apply")
+    T, H, hd, _ = fx.uniform_u32
+    got = oracle.rope_apply(fx.raw("_output_initial.bin", np.uint16), fx.input("cos_tab", np.uint16),
+                            fx.input("sin_tab", np.uint16), T, H, hd)
+    ulp = fp16_ulp_diff(got.ravel(), fx.expected(np.uint16))
+    # The fixture pins WGSL semantics: no f16/f32 rounding model gets within
+    # 16 ulp of it in the cancellation region, and WASM's three roundings
+    # (S6) land 44 ulp away there. The reference harness allows 32 ulp for
+    # this kernel and notes the absolute drift stays ~1e-3
+    # (tests/native/vulkan/conformance-all.js:34-44); the WASM semantics
+    # themselves are pinned bit-exactly by test_rope_apply_closed_form.
+    assert np.max(np.abs(f16(got.ravel()) - f16(fx.expected(np.uint16)))) <= 1e-3
+    assert np.mean(ulp <= 1.0) > 0.9
+
+
+def test_rope_tables_closed_form():
+    cfg = PF_CONFIG
+    T = 2048
+    cs, sn = oracle.rope_tables(cfg, T)
+    # float64 YARN (rope.ts:27-75)
+    hd, th, fac = 64, 150000.0, 32.0
+    i = np.arange(32)
+    pos = th ** (2 * i / hd)
+    ex, it = (1 / pos).astype(np.float32), (1 / (fac * pos)).astype(np.float32)
+    fcd = lambda r: hd * np.log(4096 / (r * 2 * np.pi)) / (2 * np.log(th))
+    lo, hi = max(fcd(32.0), 0), min(fcd(1.0), hd - 1)
+    ramp = np.clip((i - lo) / (hi - lo), 0, 1)
+    inv = (it.astype(np.float64) * ramp + ex.astype(np.float64) * (1 - ramp)).astype(np.float32)
+    ang = np.arange(T)[:, None] * inv.astype(np.float64)[None, :]
+    sc = 0.1 * np.log(fac) + 1
+    assert abs(sc - 1.3465735902799727) < 1e-15
+    assert fp16_ulp_diff(cs, fp16_ieee(np.cos(ang) * sc)).max() <= 1.0
+    assert fp16_ulp_diff(sn, fp16_ieee(np.sin(ang) * sc)).max() <= 1.0
+
+
+def test_rope_apply_closed_form():
+    T, H, hd = 50, 14, 64
+    x = synth.to_fp16_bits(synth.normal(95, T * H * hd)).reshape(T, H * hd)
+    cs, sn = oracle.rope_tables(PF_CONFIG, T)
+    got = oracle.rope_apply(x, cs, sn, T, H, hd)
+    xf = oracle.fp16_to_f32(x).reshape(T, H, 32, 2)
+    c, s = oracle.fp16_to_f32(cs)[:, None, :], oracle.fp16_to_f32(sn)[:, None, :]
+    a, b = xf[..., 0], xf[..., 1]
+    # S6: each product rounded to fp16, combined in f32, rounded again. The
+    # roundings and widenings are the (separately pinned) WASM conversions,
+    # whose subnormal handling differs from IEEE (S1, S2).
+    r16 = lambda v: oracle.fp16_to_f32(oracle.f32_to_fp16(np.asarray(v, np.float32)))
+    ac, bs, bc, as_ = r16(a * c), r16(b * s), r16(b * c), r16(a * s)
+    ref = np.stack([(ac - bs).astype(np.float32), (bc + as_).astype(np.float32)], -1).reshape(T, H * hd)
+    assert np.array_equal(got, oracle.f32_to_fp16(ref))
+
+
+# ---------------------------------------------------------------- elementwise fixtures
+
+def test_add_cast_fixtures(fixture):
+    fx = fixture("add_fp16")
+    got = oracle.add_fp16(fx.input("a", np.uint16), fx.input("b", np.uint16))
+    assert fp16_ulp_diff(got, fx.expected(np.uint16)).max() <= 1.0
+    fx = fixture("cast_f32_to_fp16_scaled")
+    scale = float(fx.raw("_uniform_scale.bin", np.float32)[0])
+    got = oracle.cast_scaled(fx.input("src", np.float32), scale)
+    assert fp16_ulp_diff(got, fx.expected(np.uint16)).max() <= 1.0
+    fx = fixture("cast_fp16_to_f32")
+    got = oracle.fp16_to_f32(fx.input("src", np.uint16))
+    assert np.array_equal(got, fx.expected(np.float32))
