@@ -1,0 +1,112 @@
+"""GPU parity of the whole forward (BASELINE config 5 path) through the
+HipBackend / C ABI, against the oracle forward on identical seeded inputs.
+
+Bars: logits within rel-err 2e-3 (normwise) and per-token argmax agreement
+>= 99.9 %. Per-layer taps are also compared block by block (oracle block fed
+the GPU's own input residual), which isolates one layer's error from the
+accumulation of the layers before it."""
+import numpy as np
+import pytest
+
+import oracle
+from parity_util import f16, rel_err_norm
+from textsift_amd import synth
+from textsift_amd.backend import HipBackend
+from textsift_amd.config import PF_CONFIG
+
+pytestmark = pytest.mark.gpu
+
+L, E, V = 2, 16, 4096
+
+
+@pytest.fixture(scope="module")
+def small():
+    w = synth.make_model_weights(PF_CONFIG, seed=11, num_layers=L, num_experts=E, vocab_size=V)
+    be = HipBackend(w)
+    be.warmup()
+    be.warmup()  # idempotent (native/backend.ts:408)
+    yield w, be
+    be.dispose()
+    be.dispose()  # safe twice
+
+
+def test_forward_contract_errors(small):
+    w, be = small
+    with pytest.raises(ValueError):
+        be.forward(np.zeros(8, np.int32), np.ones(7, np.uint8))
+    fresh = HipBackend(w)
+    with pytest.raises(RuntimeError):
+        fresh.forward(np.zeros(4, np.int32), np.ones(4, np.uint8))
+
+
+@pytest.mark.parametrize("T,masked", [(200, False), (300, True), (5, False)])
+def test_small_forward_vs_oracle(small, T, masked):
+    w, be = small
+    ids = synth.token_ids(800 + T, T, V)
+    ids[0] = V + 7  # out-of-range id -> zero embedding row (wasm_exports.zig:1545-1549)
+    mask = np.ones(T, np.uint8)
+    if masked:
+        mask[-20:] = 0
+    got = be.forward(ids, mask).as_matrix()
+    ref = f16(oracle.model_forward(PF_CONFIG, w, ids, mask=mask, num_layers=L)).astype(np.float32)
+    assert rel_err_norm(got, ref) < 2e-3
+    assert np.mean(np.argmax(got, 1) == np.argmax(ref, 1)) >= 0.999 or T < 100
+
+
+def test_batched_forward_equals_per_sequence(small):
+    """B sequences in one launch set == B separate forwards (bands and RoPE
+    positions restart per sequence)."""
+    w, be = small
+    B, T = 3, 130
+    ids = synth.token_ids(900, B * T, V).reshape(B, T)
+    got = be.forward_batch(ids)
+    for b in range(B):
+        one = be.forward(ids[b], np.ones(T, np.uint8)).as_matrix()
+        assert np.array_equal(got[b], one)
+
+
+def test_per_layer_taps_vs_oracle_block(small):
+    w, be = small
+    T = 256
+    ids = synth.token_ids(901, T, V)
+    m = be.model
+    m.enable_taps(True)
+    be.forward(ids, np.ones(T, np.uint8))
+    D = PF_CONFIG.hidden_size
+    cs, sn = oracle.rope_tables(PF_CONFIG, T)
+    h_in = oracle.embed_lookup(w["embed.int4"], w["embed.scales"], w["embed.zp"], ids, V, D)
+    import ctypes as C
+    cfg = oracle.make_config(PF_CONFIG, layers=L, experts=E, vocab=V)
+    for l in range(L):
+        keep = oracle._Keep()
+        layer = oracle.make_layer(keep, w, l)
+        out = np.empty((T, D), np.uint16)
+        rc = oracle.lib().pfo_block_forward(C.byref(cfg), C.byref(layer), h_in.ctypes.data_as(C.c_void_p),
+                                            out.ctypes.data_as(C.c_void_p), cs.ctypes.data_as(C.c_void_p),
+                                            sn.ctypes.data_as(C.c_void_p), None, T, 1)
+        assert rc == 0
+        gpu_h = m.tap(f"h.{l}", np.uint16, T * D).reshape(T, D)
+        err = rel_err_norm(f16(gpu_h), f16(out))
+        assert err < 2e-3, f"layer {l}: {err}"
+        h_in = gpu_h  # next block starts from the GPU's residual
+    m.enable_taps(False)
+
+
+@pytest.mark.parametrize("T", [2048])
+def test_full_model_forward_vs_oracle(T):
+    """BASELINE config 5 architecture at full size (8 layers, 128 experts,
+    vocab 200064), one T=2048 sequence (the reference's chunk length)."""
+    w = synth.make_model_weights(PF_CONFIG, seed=20260101)
+    be = HipBackend(w)
+    be.warmup()
+    try:
+        ids = synth.token_ids(1000, T)
+        got = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
+        ref = f16(oracle.model_forward(PF_CONFIG, w, ids, n_threads=8)).astype(np.float32)
+        err = rel_err_norm(got, ref)
+        agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
+        print(f"full model T={T}: rel-err {err:.3e}, argmax agreement {agree:.5f}")
+        assert err < 2e-3
+        assert agree >= 0.999
+    finally:
+        be.dispose()

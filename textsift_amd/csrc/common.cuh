@@ -1,0 +1,115 @@
+// common.cuh — device helpers shared by the gfx950 kernels.
+//
+// Numerics follow the reference's WASM path
+// (packages/textsift/src/zig/math.zig, zig/wasm_exports.zig): every kernel
+// is compiled with -ffp-contract=off, and the places where the reference
+// fuses a multiply-add (its relaxed_madd sites, c/fma.c:10-13) call fmaf()
+// explicitly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pf {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// fp16 bits -> f32 as zig/math.zig:45-52 computes it: exact for normals and
+// zero; subnormals / inf / NaN get the blind exponent rebias
+// (m -> 2^-15 (1 + m/1024), inf -> 65536).
+__device__ __forceinline__ float wasm_h2f(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t rest = (uint32_t)h & 0x7fffu;
+  uint32_t biased = rest == 0u ? 0u : (rest << 13) + (112u << 23);
+  return __uint_as_float(sign | biased);
+}
+
+// f32 -> fp16 bits as zig/math.zig:54-82: RNE for normal results (what the
+// hardware conversion does), round-half-up for subnormal results.
+__device__ __forceinline__ uint16_t wasm_f2h(float f) {
+  const float a = fabsf(f);
+  if (a >= 6.103515625e-05f || !(a == a)) {
+    _Float16 h = (_Float16)f;
+    uint16_t bits = __builtin_bit_cast(uint16_t, h);
+    if (!(a == a)) bits = (uint16_t)((bits & 0x8000u) | 0x7e00u);  // NaN: quiet bit (math.zig:59)
+    return bits;
+  }
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t exp32 = (u >> 23) & 0xffu;
+  int32_t e16 = (int32_t)exp32 - 127 + 15;
+  if (e16 < -10) return (uint16_t)sign;
+  uint32_t shift = (uint32_t)(14 - e16);
+  uint32_t mant24 = (u & 0x7fffffu) | 0x800000u;
+  return (uint16_t)(sign | ((mant24 + (1u << (shift - 1))) >> shift));
+}
+
+// Hardware IEEE widen (used for MFMA operands; differs from wasm_h2f only on
+// fp16 subnormals).
+__device__ __forceinline__ float hw_h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// expApproxNonPositiveF32x4 (zig/wasm_exports.zig:812-838), one lane.
+// Accuracy ~2.8e-4 relative; reproduced, not replaced, so GPU softmax and
+// SwiGLU track the reference's values.
+__device__ __forceinline__ float exp_approx(float x) {
+  const float LOG2_E = 1.44269504088896340736f;
+  float clamped = fmaxf(x, -88.0f);
+  float y = clamped * LOG2_E;
+  float fl = floorf(y);
+  int32_t iv = (int32_t)fl;
+  float frac = y - (float)iv;
+  float poly = fmaf(0.001333355f, frac, 0.009679494f);
+  poly = fmaf(poly, frac, 0.055053319f);
+  poly = fmaf(poly, frac, 0.240226522f);
+  poly = fmaf(poly, frac, 0.693154774f);
+  poly = fmaf(poly, frac, 1.000000012f);
+  float scale = __uint_as_float((uint32_t)(iv + 127) << 23);
+  return poly * scale;
+}
+
+// sigmoidF32x4 (zig/wasm_exports.zig:843-853), one lane.
+__device__ __forceinline__ float sigmoid_approx(float x) {
+  float neg_abs = fminf(x, 0.0f) - fmaxf(x, 0.0f);
+  float e = exp_approx(neg_abs);
+  float sig_neg = e / (1.0f + e);
+  return x >= 0.0f ? 1.0f - sig_neg : sig_neg;
+}
+
+// SwiGLU with clamp (zig/wasm_exports.zig:855-903 vector path).
+__device__ __forceinline__ float swiglu_clamp(float gate_raw, float up_raw) {
+  float gate = fminf(gate_raw, 7.0f);
+  float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
+  float scaled = gate * 1.702f;
+  float glu = gate * sigmoid_approx(scaled);
+  return (up + 1.0f) * glu;
+}
+
+// v_mfma_f32_16x16x32_f16 (gfx950). Operand layout (lane l, i = l / 16):
+//   a: A[m = l%16][k = 8i .. 8i+7]     (16 x 32, row-major fragment)
+//   b: B[k = 8i .. 8i+7][n = l%16]     (32 x 16)
+//   c/d: D[m = 4i + r][n = l%16], r = 0..3
+// The layout is checked on the GPU by tests/test_gpu_kernels.py
+// (probe_mfma_f16) against a host matrix product.
+__device__ __forceinline__ f4_t mfma16x16x32(h8_t a, h8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Wave-wide reductions over 64 lanes.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace pf

@@ -1,0 +1,588 @@
+// forward.cpp — the privacy-filter encoder forward on one GPU
+// (include/pfhip.h: pfhip_model_*).
+//
+// Composition follows the reference's WASM path (browser/inference/
+// model.ts:50-105, block.ts:108-197, attention.ts:45-215, expert.ts:104-212)
+// with the GPU decomposition of NodeBackend.forward
+// (native/backend.ts:433-704) collapsed into 11 launches per layer:
+//
+//   [layer 0 only] embed -> h ; rms_norm(h, ln_in) -> xn (f32)
+//   per layer l:
+//     QKV GEMM  xn -> qkv (fp16, bias, RoPE on q/k in the epilogue)
+//     banded attention qkv -> att (fp16)
+//     O GEMM    att -> o (fp16)
+//     add+rms_norm  h + o -> h2 (fp16), xn (f32)
+//     router GEMM xn -> logits (f32); top-k/softmax -> (idx, w)
+//     routing plan: count / scan / scatter (stable counting sort by expert)
+//     gate_up grouped GEMM (gathered xn rows) + SwiGLU -> glu (f32)
+//     down grouped GEMM glu -> y (f32, slot order)
+//     combine: h_next = fp16(h2 + fp16(sum_k w_k y_k)) ; xn = rms_norm(h_next, next ln)
+//   classifier GEMM xn -> fp16 logits -> f32
+//
+// B sequences of T tokens are processed together: every token-wise kernel
+// sees B*T rows; attention bands never cross a sequence boundary; RoPE
+// positions restart per sequence. Weights stay in the ONNX byte layouts;
+// finalize() concatenates q/k/v into one [1152][K] weight so the three
+// projections are one GEMM.
+#include <cmath>
+#include <cstring>
+
+#include "pfhip_internal.h"
+
+using namespace pf;
+
+namespace {
+
+struct DevT {
+  void* p = nullptr;
+  size_t n = 0;
+};
+
+struct QW {  // one MatMulNBits weight on device
+  const uint8_t* q = nullptr;
+  const uint16_t* s = nullptr;
+  const uint8_t* z = nullptr;
+  const uint16_t* bias = nullptr;
+};
+
+struct LayerW {
+  const uint16_t* ln_in;
+  const uint16_t* ln_post;
+  QW qkv, o, router, gate_up, down;
+  const float* sinks;
+};
+
+// ONNX-layout byte sizes of a MatMulNBits weight [N][K]
+size_t q_bytes(size_t N, size_t K) { return N * K / 2; }
+size_t s_bytes(size_t N, size_t K) { return N * (K / 32) * 2; }
+size_t z_bytes(size_t N, size_t K) { return N * ((K / 32 + 1) / 2); }
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct pfhip_model {
+  pfhip_backend* b = nullptr;
+  pfhip_model_config cfg{};
+  std::map<std::string, size_t> expected;   // name -> byte size
+  std::map<std::string, DevT> w;            // uploaded tensors
+  std::vector<DevT> owned;                  // derived tensors (fused qkv)
+  std::vector<LayerW> layers;
+  bool finalized = false;
+  // per-forward scratch
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  int cap_tokens = 0;
+  // RoPE tables for one sequence length
+  int rope_T = 0;
+  uint16_t* rope_cos = nullptr;
+  uint16_t* rope_sin = nullptr;
+  // host-API staging
+  pfhip_buffer* ids_buf = nullptr;
+  pfhip_buffer* mask_buf = nullptr;
+  pfhip_buffer* logits_buf = nullptr;
+  // debug taps
+  bool taps = false;
+  std::map<std::string, std::vector<uint8_t>> tap;
+};
+
+namespace {
+
+void expect(pfhip_model* m, const std::string& name, size_t bytes) { m->expected[name] = bytes; }
+
+void expect_qw(pfhip_model* m, const std::string& p, size_t N, size_t K, size_t lead = 1) {
+  expect(m, p + ".int4", lead * q_bytes(N, K));
+  expect(m, p + ".scales", lead * s_bytes(N, K));
+  expect(m, p + ".zp", lead * z_bytes(N, K));
+  expect(m, p + ".bias", lead * N * 2);
+}
+
+template <class T>
+const T* W(pfhip_model* m, const std::string& name) {
+  auto it = m->w.find(name);
+  if (it == m->w.end()) throw Error("missing weight \"" + name + "\"");
+  return static_cast<const T*>(it->second.p);
+}
+
+QW qw(pfhip_model* m, const std::string& p) {
+  return QW{W<uint8_t>(m, p + ".int4"), W<uint16_t>(m, p + ".scales"), W<uint8_t>(m, p + ".zp"),
+            W<uint16_t>(m, p + ".bias")};
+}
+
+// YARN RoPE tables (browser/inference/rope.ts:27-144): inverse frequencies
+// in f32 from float64 math, angle = t * invFreq in float64, cos/sin scaled by
+// 0.1 ln(factor) + 1, stored to f32 and then to fp16 (rope.ts:82-108).
+uint16_t f32_to_fp16_host(float f) {
+  if (f == 0.0f) return 0;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, exp32 = (u >> 23) & 0xffu, mant = u & 0x7fffffu;
+  if (exp32 == 0xffu) return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0u));
+  int e16 = (int)exp32 - 127 + 15;
+  if (e16 >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+  if (e16 <= 0) {
+    if (e16 < -10) return (uint16_t)sign;
+    const uint32_t shift = (uint32_t)(14 - e16), m24 = mant | 0x800000u;
+    return (uint16_t)(sign | ((m24 + (1u << (shift - 1))) >> shift));
+  }
+  const uint32_t lsb = (mant >> 13) & 1u;
+  uint32_t m10 = (mant + 0xfffu + lsb) >> 13;
+  uint32_t e = (uint32_t)e16;
+  if (m10 >= 0x400u) {
+    m10 = 0;
+    if (++e >= 0x1fu) return (uint16_t)(sign | 0x7c00u);
+  }
+  return (uint16_t)(sign | (e << 10) | m10);
+}
+
+void build_rope_tables(const pfhip_model_config& c, int T, std::vector<uint16_t>& cs, std::vector<uint16_t>& sn) {
+  const int hd = (int)c.head_dim, half = hd / 2;
+  std::vector<float> ex(half), in(half), inv(half);
+  for (int i = 0; i < half; ++i) {
+    const double pos = std::pow(c.rope_theta, (double)(2 * i) / (double)hd);
+    ex[i] = (float)(1.0 / pos);
+    in[i] = (float)(1.0 / (c.rope_factor * pos));
+  }
+  const double PI = 3.141592653589793;
+  double lo = ((double)hd * std::log((double)c.rope_orig_max / (c.rope_beta_fast * 2.0 * PI))) /
+              (2.0 * std::log(c.rope_theta));
+  double hi = ((double)hd * std::log((double)c.rope_orig_max / (c.rope_beta_slow * 2.0 * PI))) /
+              (2.0 * std::log(c.rope_theta));
+  if (c.rope_truncate) {
+    lo = std::floor(lo);
+    hi = std::ceil(hi);
+  }
+  lo = std::max(lo, 0.0);
+  hi = std::min(hi, (double)(hd - 1));
+  const double rmax = hi == lo ? lo + 0.001 : hi;
+  for (int i = 0; i < half; ++i) {
+    const double lin = ((double)i - lo) / (rmax - lo);
+    const double ramp = std::min(std::max(lin, 0.0), 1.0);
+    const double ef = 1.0 - ramp;
+    inv[i] = (float)((double)in[i] * (1.0 - ef) + (double)ex[i] * ef);
+  }
+  const double scaling = c.rope_factor <= 1.0 ? 1.0 : 0.1 * std::log(c.rope_factor) + 1.0;
+  cs.resize((size_t)T * half);
+  sn.resize((size_t)T * half);
+  for (int t = 0; t < T; ++t)
+    for (int i = 0; i < half; ++i) {
+      const double ang = (double)t * (double)inv[i];
+      cs[(size_t)t * half + i] = f32_to_fp16_host((float)(std::cos(ang) * scaling));
+      sn[(size_t)t * half + i] = f32_to_fp16_host((float)(std::sin(ang) * scaling));
+    }
+}
+
+struct Scr {
+  uint16_t *h0, *h1, *h2, *qkv, *att, *o, *logits16;
+  float *xn, *rlogits, *rw, *glu, *y, *logits;
+  int32_t* ridx;
+  void* plan;
+};
+
+int tile_for(int M, int K, int E) { return (M * K / E >= 256) ? 128 : 64; }
+
+size_t scratch_layout(const pfhip_model_config& c, int M, Scr* s, void* base) {
+  const size_t D = c.hidden, E = c.experts, K = c.topk, F = c.dff, C = c.classes;
+  const size_t NQKV = (size_t)(c.heads + 2 * c.kv_heads) * c.head_dim;
+  const size_t HQ = (size_t)c.heads * c.head_dim;
+  const size_t S = (size_t)M * K;
+  const int tt = tile_for(M, (int)K, (int)E);
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) -> void* {
+    void* r = p ? p + off : nullptr;
+    off += al256(bytes);
+    return r;
+  };
+  Scr t;
+  t.h0 = (uint16_t*)take((size_t)M * D * 2);
+  t.h1 = (uint16_t*)take((size_t)M * D * 2);
+  t.h2 = (uint16_t*)take((size_t)M * D * 2);
+  t.xn = (float*)take((size_t)M * D * 4);
+  t.qkv = (uint16_t*)take((size_t)M * NQKV * 2);
+  t.att = (uint16_t*)take((size_t)M * HQ * 2);
+  t.o = (uint16_t*)take((size_t)M * D * 2);
+  t.rlogits = (float*)take((size_t)M * E * 4);
+  t.ridx = (int32_t*)take(S * 4);
+  t.rw = (float*)take(S * 4);
+  t.glu = (float*)take(S * F * 4);
+  t.y = (float*)take(S * D * 4);
+  t.logits16 = (uint16_t*)take((size_t)M * C * 2);
+  t.logits = (float*)take((size_t)M * C * 4);
+  t.plan = take(moe_plan_bytes(M, (int)K, (int)E, tt));
+  if (s) *s = t;
+  return off;
+}
+
+}  // namespace
+
+namespace pf {
+void cast_f16_f32_ieee(pfhip_backend* b, const uint16_t* s, float* d, size_t n);
+}
+
+static void record_tap(pfhip_model* m, const std::string& name, const void* dev, size_t bytes) {
+  if (!m->taps) return;
+  std::vector<uint8_t>& v = m->tap[name];
+  v.resize(bytes);
+  PF_HIP(hipMemcpyAsync(v.data(), dev, bytes, hipMemcpyDeviceToHost, m->b->stream));
+  PF_HIP(hipStreamSynchronize(m->b->stream));
+}
+
+static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask, int B, int T, float* logits_out) {
+  pfhip_backend* b = m->b;
+  const pfhip_model_config& c = m->cfg;
+  const int M = B * T;
+  const int D = (int)c.hidden, E = (int)c.experts, K = (int)c.topk, F = (int)c.dff, C = (int)c.classes;
+  const int Hq = (int)c.heads, Hkv = (int)c.kv_heads, hd = (int)c.head_dim;
+  const int NQKV = (Hq + 2 * Hkv) * hd;
+  const int tt = tile_for(M, K, E);
+
+  // scratch
+  if (M > m->cap_tokens) {
+    const size_t bytes = scratch_layout(c, M, nullptr, nullptr);
+    if (m->scratch) {
+      PF_HIP(hipStreamSynchronize(b->stream));
+      PF_HIP(hipFree(m->scratch));
+      m->scratch = nullptr;
+    }
+    PF_HIP(hipMalloc(&m->scratch, bytes));
+    m->scratch_bytes = bytes;
+    m->cap_tokens = M;
+  }
+  Scr s;
+  scratch_layout(c, M, &s, m->scratch);
+  MoePlan plan = moe_plan_carve(s.plan, M, K, E, tt);
+
+  // RoPE tables (host-built, cached per sequence length)
+  if (m->rope_T != T) {
+    std::vector<uint16_t> cs, sn;
+    build_rope_tables(c, T, cs, sn);
+    if (m->rope_cos) {
+      PF_HIP(hipStreamSynchronize(b->stream));
+      hipFree(m->rope_cos);
+      hipFree(m->rope_sin);
+      m->rope_cos = m->rope_sin = nullptr;
+    }
+    PF_HIP(hipMalloc(&m->rope_cos, cs.size() * 2));
+    PF_HIP(hipMalloc(&m->rope_sin, sn.size() * 2));
+    PF_HIP(hipMemcpy(m->rope_cos, cs.data(), cs.size() * 2, hipMemcpyHostToDevice));
+    PF_HIP(hipMemcpy(m->rope_sin, sn.data(), sn.size() * 2, hipMemcpyHostToDevice));
+    m->rope_T = T;
+  }
+
+  embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
+               M, (int)c.vocab, D);
+  rms_norm_f32(b, s.h0, m->layers[0].ln_in, s.xn, M, D, c.eps);
+  uint16_t* h = s.h0;
+  uint16_t* hn = s.h1;
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const LayerW& L = m->layers[l];
+    const std::string tag = std::to_string(l);
+    {  // QKV (+bias, RoPE)
+      GemmArgs a;
+      a.x = s.xn; a.ldx = D;
+      a.w = L.qkv.q; a.ws = L.qkv.s; a.wz = L.qkv.z; a.bias = L.qkv.bias;
+      a.out = s.qkv; a.ldo = NQKV; a.M = M; a.N = NQKV; a.K = D;
+      a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
+      gemm_int4(b, a, XKind::F32, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
+    }
+    record_tap(m, "qkv." + tag, s.qkv, (size_t)M * NQKV * 2);
+    {
+      AttnArgs a{};
+      a.q = s.qkv; a.q_stride = NQKV;
+      a.k = s.qkv + Hq * hd; a.k_stride = NQKV;
+      a.v = s.qkv + (Hq + Hkv) * hd; a.v_stride = NQKV;
+      a.sinks = L.sinks; a.mask = mask;
+      a.out = s.att; a.out_stride = Hq * hd;
+      a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.head_dim = hd; a.window = (int)c.window; a.scale = 1.0f;
+      banded_attention(b, a);
+    }
+    record_tap(m, "att." + tag, s.att, (size_t)M * Hq * hd * 2);
+    {
+      GemmArgs a;
+      a.x = s.att; a.ldx = Hq * hd;
+      a.w = L.o.q; a.ws = L.o.s; a.wz = L.o.z; a.bias = L.o.bias;
+      a.out = s.o; a.ldo = D; a.M = M; a.N = D; a.K = Hq * hd;
+      gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
+    }
+    add_rms_norm_f32(b, h, s.o, L.ln_post, s.h2, s.xn, M, D, c.eps);
+    record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
+    {
+      GemmArgs a;
+      a.x = s.xn; a.ldx = D;
+      a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
+      a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
+      gemm_int4(b, a, XKind::F32, Epi::F32, false, 128, "gemm_router");
+    }
+    router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
+    record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
+    record_tap(m, "ridx." + tag, s.ridx, (size_t)M * K * 4);
+    record_tap(m, "rw." + tag, s.rw, (size_t)M * K * 4);
+    moe_route(b, s.ridx, M, K, E, plan);
+    {
+      GemmArgs g;
+      g.x = s.xn; g.ldx = D; g.row_map = plan.slot_token;
+      g.w = L.gate_up.q; g.ws = L.gate_up.s; g.wz = L.gate_up.z; g.bias = L.gate_up.bias;
+      g.w_gs = q_bytes(2 * F, D); g.ws_gs = s_bytes(2 * F, D) / 2; g.wz_gs = z_bytes(2 * F, D);
+      g.bias_gs = (size_t)2 * F;
+      g.out = s.glu; g.ldo = F; g.M = M * K; g.N = 2 * F; g.K = D;
+      g.tiles = plan.tiles; g.num_tiles = plan.num_tiles; g.max_tiles = plan.max_tiles;
+      gemm_int4(b, g, XKind::F32, Epi::SWIGLU_F32, true, tt, "gemm_moe_gate_up");
+    }
+    {
+      GemmArgs d;
+      d.x = s.glu; d.ldx = F;
+      d.w = L.down.q; d.ws = L.down.s; d.wz = L.down.z; d.bias = L.down.bias;
+      d.w_gs = q_bytes(D, F); d.ws_gs = s_bytes(D, F) / 2; d.wz_gs = z_bytes(D, F); d.bias_gs = (size_t)D;
+      d.out = s.y; d.ldo = D; d.M = M * K; d.N = D; d.K = F;
+      d.tiles = plan.tiles; d.num_tiles = plan.num_tiles; d.max_tiles = plan.max_tiles;
+      gemm_int4(b, d, XKind::F32, Epi::F32, true, tt, "gemm_moe_down");
+    }
+    const uint16_t* gamma_next = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : W<uint16_t>(m, "final_norm");
+    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn, M, K, D, c.eps);
+    record_tap(m, "h." + tag, hn, (size_t)M * D * 2);
+    std::swap(h, hn);
+  }
+  {
+    GemmArgs a;
+    a.x = s.xn; a.ldx = D;
+    QW sc = qw(m, "score");
+    a.w = sc.q; a.ws = sc.s; a.wz = sc.z; a.bias = sc.bias;
+    a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
+    gemm_int4(b, a, XKind::F32, Epi::F16, false, 128, "gemm_classifier");
+  }
+  record_tap(m, "logits16", s.logits16, (size_t)M * C * 2);
+  // wasm.ts:776-796 widens the fp16 logits IEEE-correctly
+  cast_f16_f32_ieee(b, s.logits16, logits_out ? logits_out : s.logits, (size_t)M * C);
+}
+
+extern "C" {
+
+pfhip_model* pfhip_model_create(pfhip_backend* b, const pfhip_model_config* cfg, char* err, size_t cap) {
+  try {
+    PF_CHECK(b && cfg, "null argument");
+    const pfhip_model_config& c = *cfg;
+    PF_CHECK(c.hidden % 32 == 0 && c.dff % 32 == 0 && c.hidden <= 1024, "hidden and dff must be multiples of 32");
+    PF_CHECK(c.head_dim == 64, "head_dim must be 64");
+    PF_CHECK(c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
+    PF_CHECK(c.topk >= 1 && c.topk <= 8 && c.experts >= c.topk && c.experts <= 256, "bad experts / topk");
+    PF_CHECK(c.layers >= 1 && c.classes >= 1 && c.vocab >= 1, "bad layers / classes / vocab");
+    PF_CHECK(c.window <= 128, "window must be <= 128");
+    pfhip_model* m = new pfhip_model();
+    m->b = b;
+    m->cfg = c;
+    const size_t D = c.hidden, Hq = c.heads, Hkv = c.kv_heads, hd = c.head_dim, E = c.experts, F = c.dff;
+    expect(m, "embed.int4", q_bytes(c.vocab, D));
+    expect(m, "embed.scales", s_bytes(c.vocab, D));
+    expect(m, "embed.zp", z_bytes(c.vocab, D));
+    for (uint32_t l = 0; l < c.layers; ++l) {
+      const std::string p = "layers." + std::to_string(l) + ".";
+      expect(m, p + "input_layernorm", D * 2);
+      expect(m, p + "post_attention_layernorm", D * 2);
+      expect_qw(m, p + "attn.q_proj", Hq * hd, D);
+      expect_qw(m, p + "attn.k_proj", Hkv * hd, D);
+      expect_qw(m, p + "attn.v_proj", Hkv * hd, D);
+      expect_qw(m, p + "attn.o_proj", D, Hq * hd);
+      expect(m, p + "attn.sinks", Hq * 4);
+      expect_qw(m, p + "router", E, D);
+      expect_qw(m, p + "experts.gate_up", 2 * F, D, E);
+      expect_qw(m, p + "experts.down", D, F, E);
+    }
+    expect(m, "final_norm", D * 2);
+    expect_qw(m, "score", c.classes, D);
+    return m;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return nullptr;
+  }
+}
+
+void pfhip_model_destroy(pfhip_model* m) {
+  if (!m) return;
+  hipStreamSynchronize(m->b->stream);
+  for (auto& kv : m->w) hipFree(kv.second.p);
+  for (auto& t : m->owned) hipFree(t.p);
+  if (m->scratch) hipFree(m->scratch);
+  if (m->rope_cos) hipFree(m->rope_cos);
+  if (m->rope_sin) hipFree(m->rope_sin);
+  pfhip_release_buffer(m->b, m->ids_buf);
+  pfhip_release_buffer(m->b, m->mask_buf);
+  pfhip_release_buffer(m->b, m->logits_buf);
+  delete m;
+}
+
+int pfhip_model_set_weight(pfhip_model* m, const char* name, const void* bytes, size_t n, char* err, size_t cap) {
+  try {
+    PF_CHECK(m && name && bytes, "null argument");
+    auto it = m->expected.find(name);
+    PF_CHECK(it != m->expected.end(), std::string("unexpected weight \"") + name + "\"");
+    // NodeBackend pads uploads to a multiple of 4 bytes (native/backend.ts:152-160)
+    PF_CHECK(n >= it->second && n <= ((it->second + 3) & ~(size_t)3),
+             std::string("weight \"") + name + "\" has " + std::to_string(n) + " bytes, expected " +
+                 std::to_string(it->second));
+    auto& t = m->w[name];
+    if (t.p && t.n < n) {
+      hipFree(t.p);
+      t.p = nullptr;
+    }
+    if (!t.p) PF_HIP(hipMalloc(&t.p, al256(n)));
+    t.n = n;
+    PF_HIP(hipMemcpy(t.p, bytes, n, hipMemcpyHostToDevice));
+    m->finalized = false;
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_model_finalize(pfhip_model* m, char* err, size_t cap) {
+  try {
+    PF_CHECK(m, "null model");
+    for (auto& kv : m->expected)
+      PF_CHECK(m->w.count(kv.first), "missing weight \"" + kv.first + "\"");
+    const pfhip_model_config& c = m->cfg;
+    const size_t D = c.hidden, hd = c.head_dim;
+    const size_t Nq = c.heads * hd, Nk = c.kv_heads * hd;
+    for (auto& t : m->owned) hipFree(t.p);
+    m->owned.clear();
+    m->layers.clear();
+    for (uint32_t l = 0; l < c.layers; ++l) {
+      const std::string p = "layers." + std::to_string(l) + ".";
+      LayerW L;
+      L.ln_in = W<uint16_t>(m, p + "input_layernorm");
+      L.ln_post = W<uint16_t>(m, p + "post_attention_layernorm");
+      // fused q|k|v weight: rows stacked along N
+      DevT fq, fs, fz, fb;
+      const size_t N = Nq + 2 * Nk;
+      PF_HIP(hipMalloc(&fq.p, q_bytes(N, D)));
+      PF_HIP(hipMalloc(&fs.p, s_bytes(N, D)));
+      PF_HIP(hipMalloc(&fz.p, z_bytes(N, D)));
+      PF_HIP(hipMalloc(&fb.p, N * 2));
+      size_t row = 0;
+      for (auto& nm : {std::make_pair("q_proj", Nq), std::make_pair("k_proj", Nk), std::make_pair("v_proj", Nk)}) {
+        const std::string wp = p + "attn." + nm.first;
+        const size_t n = nm.second;
+        PF_HIP(hipMemcpy((char*)fq.p + q_bytes(row, D), W<uint8_t>(m, wp + ".int4"), q_bytes(n, D),
+                         hipMemcpyDeviceToDevice));
+        PF_HIP(hipMemcpy((char*)fs.p + s_bytes(row, D), W<uint16_t>(m, wp + ".scales"), s_bytes(n, D),
+                         hipMemcpyDeviceToDevice));
+        PF_HIP(hipMemcpy((char*)fz.p + z_bytes(row, D), W<uint8_t>(m, wp + ".zp"), z_bytes(n, D),
+                         hipMemcpyDeviceToDevice));
+        PF_HIP(hipMemcpy((char*)fb.p + row * 2, W<uint16_t>(m, wp + ".bias"), n * 2, hipMemcpyDeviceToDevice));
+        row += n;
+      }
+      m->owned.push_back(fq);
+      m->owned.push_back(fs);
+      m->owned.push_back(fz);
+      m->owned.push_back(fb);
+      L.qkv = QW{(const uint8_t*)fq.p, (const uint16_t*)fs.p, (const uint8_t*)fz.p, (const uint16_t*)fb.p};
+      L.o = qw(m, p + "attn.o_proj");
+      L.router = qw(m, p + "router");
+      L.gate_up = qw(m, p + "experts.gate_up");
+      L.down = qw(m, p + "experts.down");
+      L.sinks = W<float>(m, p + "attn.sinks");
+      m->layers.push_back(L);
+    }
+    m->finalized = true;
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_model_enable_taps(pfhip_model* m, int on) {
+  if (!m) return -1;
+  m->taps = on != 0;
+  if (!m->taps) m->tap.clear();
+  return 0;
+}
+
+int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* mask, uint32_t batch,
+                               uint32_t seq_len, pfhip_buffer* logits, char* err, size_t cap) {
+  try {
+    PF_CHECK(m && ids && logits, "null argument");
+    PF_CHECK(m->finalized, "call pfhip_model_finalize() first");
+    PF_CHECK(batch >= 1 && seq_len >= 1, "batch and seq_len must be positive");
+    const size_t M = (size_t)batch * seq_len;
+    PF_CHECK(M <= (1u << 22), "batch * seq_len too large");
+    PF_CHECK(ids->size >= M * 4, "ids buffer too small");
+    PF_CHECK(!mask || mask->size >= M, "mask buffer too small");
+    PF_CHECK(logits->size >= M * m->cfg.classes * 4, "logits buffer too small");
+    PF_HIP(hipSetDevice(m->b->device));
+    run_forward(m, static_cast<const int32_t*>(ids->ptr), mask ? static_cast<const uint8_t*>(mask->ptr) : nullptr,
+                (int)batch, (int)seq_len, static_cast<float*>(logits->ptr));
+    PF_HIP(hipStreamSynchronize(m->b->stream));
+    prof_flush(m->b);
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_model_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask, uint32_t batch, uint32_t seq_len,
+                        float* logits, char* err, size_t cap) {
+  try {
+    PF_CHECK(m && ids && logits, "null argument");
+    PF_CHECK(batch >= 1 && seq_len >= 1, "batch and seq_len must be positive");
+    const size_t M = (size_t)batch * seq_len;
+    char e2[PFHIP_ERR_CAP];
+    auto ensure = [&](pfhip_buffer*& buf, size_t bytes) {
+      if (!buf || buf->size < bytes) {
+        pfhip_release_buffer(m->b, buf);
+        buf = pfhip_create_empty_buffer(m->b, bytes, e2, sizeof e2);
+        PF_CHECK(buf, e2);
+      }
+    };
+    ensure(m->ids_buf, M * 4);
+    ensure(m->logits_buf, M * m->cfg.classes * 4);
+    PF_CHECK(pfhip_write_buffer(m->b, m->ids_buf, 0, ids, M * 4, e2, sizeof e2) == 0, e2);
+    // wasm.ts:753-764: an all-ones mask is elided
+    bool use_mask = false;
+    if (mask)
+      for (size_t i = 0; i < M; ++i)
+        if (mask[i] != 1) {
+          use_mask = true;
+          break;
+        }
+    if (use_mask) {
+      ensure(m->mask_buf, M);
+      PF_CHECK(pfhip_write_buffer(m->b, m->mask_buf, 0, mask, M, e2, sizeof e2) == 0, e2);
+    }
+    PF_CHECK(pfhip_model_forward_device(m, m->ids_buf, use_mask ? m->mask_buf : nullptr, batch, seq_len,
+                                        m->logits_buf, e2, sizeof e2) == 0,
+             e2);
+    PF_CHECK(pfhip_read_buffer(m->b, m->logits_buf, 0, logits, M * m->cfg.classes * 4, e2, sizeof e2) == 0, e2);
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_model_read_tap(pfhip_model* m, const char* name, void* dst, size_t n, char* err, size_t cap) {
+  try {
+    PF_CHECK(m && name && dst, "null argument");
+    auto it = m->tap.find(name);
+    PF_CHECK(it != m->tap.end(), std::string("no tap \"") + name + "\" (enable taps before the forward)");
+    PF_CHECK(n <= it->second.size(), "tap read larger than the tap");
+    memcpy(dst, it->second.data(), n);
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_rope_tables(const pfhip_model_config* cfg, uint32_t T, uint16_t* cos_t, uint16_t* sin_t) {
+  if (!cfg || !cos_t || !sin_t) return -1;
+  std::vector<uint16_t> cs, sn;
+  build_rope_tables(*cfg, (int)T, cs, sn);
+  memcpy(cos_t, cs.data(), cs.size() * 2);
+  memcpy(sin_t, sn.data(), sn.size() * 2);
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,387 @@
+// gemm_int4.hip — MatMulNBits int4 GEMM for gfx950 (fp16 MFMA, f32 accumulate).
+//
+// Computes out[t][n] = sum_b scale[n][b] * sum_{k in b} x[t][k] * (q[n][k] - zp[n][b]) + bias[n]
+// over the ONNX MatMulNBits layout (uint4 packed two per byte along K, low
+// nibble first; fp16 scales [N][K/32]; packed uint4 zero-points
+// [N][ceil(K/64)], even block in the low nibble) — the semantics of
+// matmulInt4BlockImpl, packages/textsift/src/zig/wasm_exports.zig:560-707.
+//
+// Mapping to CDNA4:
+//  * One v_mfma_f32_16x16x32_f16 K-step is exactly one 32-wide quant block.
+//    Weights enter the MFMA as the exact small integers (q - zp) in fp16, so
+//    every product is exact; the block's f32 partial sum is then scaled with
+//    one fmaf per accumulator, as the reference scales per block.
+//  * The GEMM is computed transposed (D = W . X^T): the MFMA's M dimension
+//    runs over weight rows, so each lane ends up holding 4 consecutive output
+//    columns of one token. That makes the epilogues lane-local: RoPE pairs
+//    (2p, 2p+1) and SwiGLU's interleaved (gate, up) columns sit in one lane,
+//    and stores are 8-16 byte vectors.
+//  * f32 activations (the WASM path feeds f32 to Q/K/V, router and experts,
+//    browser/inference/block.ts:126-176) enter as an exact fp16 hi + lo pair
+//    (two MFMAs into the same block partial), carrying 22 significant bits.
+//  * Workgroup tile: 128 weight rows x BT tokens, K staged 64 at a time
+//    through LDS (W dequantised once per workgroup, X split once), global
+//    loads for the next stage issued before the current stage's MFMAs.
+//  * Workgroup ids are remapped so each XCD walks a contiguous range of
+//    (token tile, n tile) pairs: the n tiles of one token tile share an L2.
+//  * Grouped mode: tiles come from a device list of (expert, row0, rows)
+//    built by the MoE routing kernels; weights are offset per expert and
+//    activation rows may be gathered through row_map.
+#include "common.cuh"
+#include "pfhip_internal.h"
+
+namespace pf {
+
+namespace {
+
+constexpr int BN = 128;         // weight rows (output columns) per workgroup
+constexpr int BK = 64;          // K per LDS stage = two quant blocks
+constexpr int LDW = BK + 8;     // padded LDS row (halves)
+
+// 8 nibbles of one dword -> 8 exact fp16 values (q - zp), natural k order.
+__device__ __forceinline__ u4_t dequant8(uint32_t w, uint32_t zp_pair) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;          // k0 k2 k4 k6
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // k1 k3 k5 k7
+  u4_t r;
+  r.x = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u;  // 1024+k0, 1024+k1
+  r.y = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u;
+  r.z = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u;
+  r.w = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u;
+  const h2_t off = __builtin_bit_cast(h2_t, zp_pair);  // (1024+zp, 1024+zp)
+  r.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.x) - off);
+  r.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.y) - off);
+  r.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.z) - off);
+  r.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.w) - off);
+  return r;
+}
+
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int per = total >> 3, rem = total & 7;
+  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+template <int BT, bool SPLIT, Epi EPI, bool GROUPED>
+__global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
+  constexpr int NPL = SPLIT ? 2 : 1;
+  constexpr int WT = BT / 2;   // tokens per wave
+  constexpr int WN = BN / 2;   // weight rows per wave
+  constexpr int TI = WN / 16;  // n sub-tiles per wave
+  constexpr int TJ = WT / 16;  // token sub-tiles per wave
+  // X loader geometry
+  constexpr int XCH = SPLIT ? 16 : 8;            // 16-byte chunks per row per stage
+  constexpr int XRP = 256 / XCH;                 // rows per pass
+  constexpr int XPASS = BT / XRP;                // passes
+
+  __shared__ __attribute__((aligned(16))) _Float16 Wl[BN * LDW];
+  __shared__ __attribute__((aligned(16))) float Sl[2 * BN];
+  __shared__ __attribute__((aligned(16))) _Float16 Xl[NPL * BT * LDW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wn = (wave & 1) * WN;
+  const int wt = (wave >> 1) * WT;
+  const int l16 = lane & 15, lg = lane >> 4;
+
+  const int n_tiles = (p.N + BN - 1) / BN;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int nt = bid % n_tiles;
+  const int tt = bid / n_tiles;
+  int expert = 0, row0, rows;
+  if constexpr (GROUPED) {
+    if (tt >= *p.num_tiles) return;
+    const int4 ti = reinterpret_cast<const int4*>(p.tiles)[tt];
+    expert = ti.x;
+    row0 = ti.y;
+    rows = ti.z;
+  } else {
+    row0 = tt * BT;
+    rows = min(BT, p.M - row0);
+    if (rows <= 0) return;
+  }
+  const int n0 = nt * BN;
+  const int K = p.K;
+  const int nb = K >> 5;
+  const int zstride = (nb + 1) >> 1;
+  const uint8_t* __restrict__ W = p.w + (size_t)expert * p.w_gs;
+  const uint16_t* __restrict__ WS = p.ws + (size_t)expert * p.ws_gs;
+  const uint8_t* __restrict__ WZ = p.wz ? p.wz + (size_t)expert * p.wz_gs : nullptr;
+
+  // ---- loader roles
+  const int wr = tid >> 1, wb = tid & 1;       // W: row, block within stage
+  const int wrow = n0 + wr;
+  const bool w_ok = wrow < p.N;
+  const uint8_t* wsrc = W + (size_t)wrow * (K >> 1);
+
+  const int xr = tid / XCH, xc = tid % XCH;
+  int xoff[XPASS];                              // element offset of each X row, -1 = zero row
+#pragma unroll
+  for (int i = 0; i < XPASS; ++i) {
+    const int r = xr + i * XRP;
+    if (r < rows) {
+      const int lr = row0 + r;
+      const int g = p.row_map ? p.row_map[lr] : lr;
+      xoff[i] = g * p.ldx;
+    } else {
+      xoff[i] = -1;
+    }
+  }
+
+  // ---- prefetch registers
+  u4_t wreg;
+  uint32_t zreg;   // packed (1024+zp) pair
+  float sreg;
+  u4_t xreg[XPASS];
+
+  auto load_stage = [&](int s) {
+    const int kb = s * 2 + wb;
+    if (w_ok && kb < nb) {
+      wreg = *reinterpret_cast<const u4_t*>(wsrc + kb * 16);
+      sreg = wasm_h2f(WS[(size_t)wrow * nb + kb]);
+      uint32_t zp = 0;
+      if (WZ) {
+        const uint8_t zb = WZ[(size_t)wrow * zstride + (kb >> 1)];
+        zp = (kb & 1) ? (zb >> 4) : (zb & 0xF);
+      }
+      const uint32_t hz = 0x6400u + zp;  // fp16 bits of 1024 + zp
+      zreg = hz | (hz << 16);
+    } else {
+      wreg = u4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+      zreg = 0x64086408u;  // (q - 8) with q = 8 -> exact zeros
+      sreg = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < XPASS; ++i) {
+      const int k = s * BK + xc * (SPLIT ? 4 : 8);
+      if (xoff[i] >= 0 && k < K) {
+        if constexpr (SPLIT)
+          xreg[i] = *reinterpret_cast<const u4_t*>(static_cast<const float*>(p.x) + xoff[i] + k);
+        else
+          xreg[i] = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(p.x) + xoff[i] + k);
+      } else {
+        xreg[i] = u4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  auto store_stage = [&]() {
+    // W: 32 nibbles -> 32 exact fp16 at Wl[wr][wb*32 ...]
+    u4_t* wdst = reinterpret_cast<u4_t*>(&Wl[wr * LDW + wb * 32]);
+    wdst[0] = dequant8(wreg.x, zreg);
+    wdst[1] = dequant8(wreg.y, zreg);
+    wdst[2] = dequant8(wreg.z, zreg);
+    wdst[3] = dequant8(wreg.w, zreg);
+    Sl[wb * BN + wr] = sreg;
+#pragma unroll
+    for (int i = 0; i < XPASS; ++i) {
+      const int r = xr + i * XRP;
+      if constexpr (SPLIT) {
+        const f4_t v = __builtin_bit_cast(f4_t, xreg[i]);
+        h4_t hi, lo;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          hi[c] = (_Float16)v[c];
+          lo[c] = (_Float16)(v[c] - (float)hi[c]);
+        }
+        *reinterpret_cast<h4_t*>(&Xl[r * LDW + xc * 4]) = hi;
+        *reinterpret_cast<h4_t*>(&Xl[BT * LDW + r * LDW + xc * 4]) = lo;
+      } else {
+        *reinterpret_cast<u4_t*>(&Xl[r * LDW + xc * 8]) = xreg[i];
+      }
+    }
+  };
+
+  f4_t acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int S = (nb + 1) >> 1;
+  load_stage(0);
+  for (int s = 0; s < S; ++s) {
+    if (s > 0) __syncthreads();
+    store_stage();
+    __syncthreads();
+    if (s + 1 < S) load_stage(s + 1);
+    const int nblk = min(2, nb - 2 * s);
+    for (int b = 0; b < nblk; ++b) {
+      h8_t wf[TI], xh[TJ], xl[TJ];
+      f4_t sc[TI];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        wf[i] = *reinterpret_cast<const h8_t*>(&Wl[(wn + 16 * i + l16) * LDW + b * 32 + 8 * lg]);
+        sc[i] = *reinterpret_cast<const f4_t*>(&Sl[b * BN + wn + 16 * i + 4 * lg]);
+      }
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        xh[j] = *reinterpret_cast<const h8_t*>(&Xl[(wt + 16 * j + l16) * LDW + b * 32 + 8 * lg]);
+        if constexpr (SPLIT)
+          xl[j] = *reinterpret_cast<const h8_t*>(&Xl[BT * LDW + (wt + 16 * j + l16) * LDW + b * 32 + 8 * lg]);
+      }
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          f4_t t = mfma16x16x32(wf[i], xh[j], f4_t{0.f, 0.f, 0.f, 0.f});
+          if constexpr (SPLIT) t = mfma16x16x32(wf[i], xl[j], t);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(t[r], sc[i][r], acc[i][j][r]);
+        }
+    }
+  }
+
+  // ---- epilogue: lane holds out[token = wt+16j+l16][n = wn+16i+4lg+r]
+  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const int n = n0 + wn + 16 * i + 4 * lg;
+    float bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[r] = (BIAS && n + r < p.N) ? wasm_h2f(BIAS[n + r]) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int lt = wt + 16 * j + l16;
+      if (lt >= rows) continue;
+      const size_t orow = (size_t)(row0 + lt);
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bv[r];
+      if constexpr (EPI == Epi::F32) {
+        float* o = static_cast<float*>(p.out) + orow * p.ldo + n;
+        if (n + 3 < p.N) {
+          *reinterpret_cast<f4_t*>(o) = f4_t{v[0], v[1], v[2], v[3]};
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) o[r] = v[r];
+        }
+      } else if constexpr (EPI == Epi::F16 || EPI == Epi::ROPE_F16) {
+        uint16_t hb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hb[r] = wasm_f2h(v[r]);
+        if constexpr (EPI == Epi::ROPE_F16) {
+          if (n < p.rope_cols) {
+            // rope_apply (zig/wasm_exports.zig:1460-1502) on the fp16 values:
+            // each product rounded to fp16, combined in f32, rounded again.
+            const int pos = (int)(orow % (size_t)p.seq_len);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int pidx = ((n & 63) >> 1) + h;
+              const float c = wasm_h2f(p.rope_cos[pos * 32 + pidx]);
+              const float s = wasm_h2f(p.rope_sin[pos * 32 + pidx]);
+              const float a = wasm_h2f(hb[2 * h]), bb = wasm_h2f(hb[2 * h + 1]);
+              const float ac = wasm_h2f(wasm_f2h(a * c)), bs = wasm_h2f(wasm_f2h(bb * s));
+              const float bc = wasm_h2f(wasm_f2h(bb * c)), as_ = wasm_h2f(wasm_f2h(a * s));
+              hb[2 * h] = wasm_f2h(ac - bs);
+              hb[2 * h + 1] = wasm_f2h(bc + as_);
+            }
+          }
+        }
+        uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
+        if (n + 3 < p.N) {
+          *reinterpret_cast<u2_t*>(o) = u2_t{(uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
+                                             (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) o[r] = hb[r];
+        }
+      } else {  // SwiGLU: (gate, up) interleaved columns -> glu column n/2
+        const float g0 = swiglu_clamp(v[0], v[1]);
+        const float g1 = swiglu_clamp(v[2], v[3]);
+        const size_t oc = (size_t)(n >> 1);
+        if constexpr (EPI == Epi::SWIGLU_F32) {
+          float* o = static_cast<float*>(p.out) + orow * p.ldo + oc;
+          *reinterpret_cast<float2*>(o) = make_float2(g0, g1);
+        } else {
+          uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
+          *reinterpret_cast<uint32_t*>(o) = (uint32_t)wasm_f2h(g0) | ((uint32_t)wasm_f2h(g1) << 16);
+        }
+      }
+    }
+  }
+}
+
+template <int BT, bool SPLIT, Epi EPI, bool GROUPED>
+void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
+  const int n_tiles = (a.N + BN - 1) / BN;
+  const int t_tiles = GROUPED ? a.max_tiles : (a.M + BT - 1) / BT;
+  const long grid = (long)n_tiles * t_tiles;
+  if (grid == 0) return;
+  PF_CHECK(grid < (1L << 31), "gemm_int4: grid too large");
+  ProfScope ps(b, name);
+  hipLaunchKernelGGL((k_gemm_int4<BT, SPLIT, EPI, GROUPED>), dim3((unsigned)grid), dim3(256), 0, b->stream, a);
+  PF_HIP(hipGetLastError());
+}
+
+template <int BT, bool SPLIT, bool GROUPED>
+void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name) {
+  switch (epi) {
+    case Epi::F16: return launch<BT, SPLIT, Epi::F16, GROUPED>(b, a, name);
+    case Epi::F32: return launch<BT, SPLIT, Epi::F32, GROUPED>(b, a, name);
+    case Epi::ROPE_F16: return launch<BT, SPLIT, Epi::ROPE_F16, GROUPED>(b, a, name);
+    case Epi::SWIGLU_F32: return launch<BT, SPLIT, Epi::SWIGLU_F32, GROUPED>(b, a, name);
+    case Epi::SWIGLU_F16: return launch<BT, SPLIT, Epi::SWIGLU_F16, GROUPED>(b, a, name);
+  }
+}
+
+}  // namespace
+
+void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
+               const char* prof_name) {
+  PF_CHECK(a.K > 0 && a.K % 32 == 0, "gemm_int4: K must be a positive multiple of 32");
+  PF_CHECK(a.N > 0, "gemm_int4: N must be positive");
+  PF_CHECK(a.x && a.w && a.ws && a.out, "gemm_int4: null operand");
+  const int xalign = xk == XKind::F32 ? 4 : 8;  // 16-byte vector loads
+  PF_CHECK(a.ldx % xalign == 0 && a.K % 8 == 0, "gemm_int4: activation row stride must allow 16-byte loads");
+  PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
+           "gemm_int4: activations and weights must be 16-byte aligned");
+  PF_CHECK(a.K / 2 % 16 == 0, "gemm_int4: packed weight rows must be 16-byte multiples");
+  if (epi == Epi::SWIGLU_F32 || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_int4: SwiGLU needs N % 4 == 0");
+  if (epi == Epi::ROPE_F16)
+    PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
+             "gemm_int4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
+  if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_int4: grouped mode needs a tile list");
+  else PF_CHECK(a.M >= 0, "gemm_int4: M must be non-negative");
+  const bool split = xk == XKind::F32;
+  if (tile_t == 64) {
+    if (split) {
+      if (grouped) dispatch_epi<64, true, true>(b, a, epi, prof_name);
+      else dispatch_epi<64, true, false>(b, a, epi, prof_name);
+    } else {
+      if (grouped) dispatch_epi<64, false, true>(b, a, epi, prof_name);
+      else dispatch_epi<64, false, false>(b, a, epi, prof_name);
+    }
+  } else {
+    PF_CHECK(tile_t == 128, "gemm_int4: tile_t must be 64 or 128");
+    if (split) {
+      if (grouped) dispatch_epi<128, true, true>(b, a, epi, prof_name);
+      else dispatch_epi<128, true, false>(b, a, epi, prof_name);
+    } else {
+      if (grouped) dispatch_epi<128, false, true>(b, a, epi, prof_name);
+      else dispatch_epi<128, false, false>(b, a, epi, prof_name);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- layout probe
+
+__global__ void k_probe_mfma(const uint16_t* A, const uint16_t* B, float* D) {
+  // A: 16x32 row-major fp16, B: 32x16 row-major fp16, D: 16x16 row-major f32
+  const int l = threadIdx.x, l16 = l & 15, lg = l >> 4;
+  h8_t a, bb;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = __builtin_bit_cast(_Float16, A[l16 * 32 + 8 * lg + i]);
+    bb[i] = __builtin_bit_cast(_Float16, B[(8 * lg + i) * 16 + l16]);
+  }
+  f4_t d = mfma16x16x32(a, bb, f4_t{0.f, 0.f, 0.f, 0.f});
+  for (int r = 0; r < 4; ++r) D[(4 * lg + r) * 16 + l16] = d[r];
+}
+
+void probe_mfma_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bm, float* d) {
+  ProfScope ps(b, "probe_mfma_f16");
+  hipLaunchKernelGGL(k_probe_mfma, dim3(1), dim3(64), 0, b->stream, a, bm, d);
+  PF_HIP(hipGetLastError());
+}
+
+}  // namespace pf

@@ -1,0 +1,184 @@
+// pfhip_internal.h — host-side structures shared by the runtime, the kernel
+// launchers and the forward orchestration.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/pfhip.h"
+
+struct pfhip_buffer {
+  void* ptr = nullptr;
+  size_t size = 0;
+  pfhip_backend* owner = nullptr;
+};
+
+namespace pf {
+
+struct Error : std::runtime_error {
+  explicit Error(const std::string& m) : std::runtime_error(m) {}
+};
+
+#define PF_HIP(expr)                                                                              \
+  do {                                                                                            \
+    hipError_t e_ = (expr);                                                                       \
+    if (e_ != hipSuccess)                                                                         \
+      throw ::pf::Error(std::string(#expr) + " failed: " + hipGetErrorString(e_) + " (" __FILE__ \
+                        ":" + std::to_string(__LINE__) + ")");                                    \
+  } while (0)
+
+#define PF_CHECK(cond, msg)                       \
+  do {                                            \
+    if (!(cond)) throw ::pf::Error(std::string(msg)); \
+  } while (0)
+
+struct ProfPending {
+  const char* name;
+  hipEvent_t start, stop;
+};
+
+}  // namespace pf
+
+struct pfhip_backend {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string device_name;
+  bool encoder_open = false;
+  // profiling
+  bool profiling = false;
+  std::vector<pf::ProfPending> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::map<std::string, std::pair<long, double>> prof;  // name -> (launches, total ms)
+  std::string report;
+};
+
+struct pfhip_encoder {
+  pfhip_backend* b = nullptr;
+  int dispatches = 0;
+};
+
+namespace pf {
+
+// Brackets one kernel launch with events when profiling is on.
+struct ProfScope {
+  pfhip_backend* b;
+  const char* name;
+  hipEvent_t start = nullptr, stop = nullptr;
+  ProfScope(pfhip_backend* b_, const char* n);
+  ~ProfScope() noexcept(false);
+};
+
+void prof_flush(pfhip_backend* b);  // synchronises and accumulates pending events
+
+void set_err(char* err, size_t cap, const std::string& msg);
+
+// ---------------------------------------------------------------- kernels
+// Launchers live in the .hip translation units; every one launches on
+// b->stream, validates its shapes on the host first and throws pf::Error.
+
+// MatMulNBits int4 GEMM.
+enum class XKind { F16, F32 };
+enum class Epi { F16, F32, ROPE_F16, SWIGLU_F32, SWIGLU_F16 };
+
+struct GemmArgs {
+  const void* x = nullptr;       // activations [rows][K] (fp16 or f32)
+  int ldx = 0;                   // row stride in elements
+  const int32_t* row_map = nullptr;  // optional gather: logical row r reads x row row_map[r]
+  const uint8_t* w = nullptr;    // [N][K/2] uint4 (per group stride w_gs bytes)
+  const uint16_t* ws = nullptr;  // [N][K/32] fp16 scales
+  const uint8_t* wz = nullptr;   // [N][ceil(K/64)] packed uint4 zero-points, NULL = 0
+  const uint16_t* bias = nullptr;  // [N] fp16, NULL = 0
+  size_t w_gs = 0, ws_gs = 0, wz_gs = 0, bias_gs = 0;  // per-expert strides (elements)
+  void* out = nullptr;
+  int ldo = 0;
+  int M = 0, N = 0, K = 0;
+  // grouped (per-expert) mode
+  const int32_t* tiles = nullptr;      // [max_tiles][4] = (expert, row0, rows, 0)
+  const int32_t* num_tiles = nullptr;  // device scalar
+  int max_tiles = 0;
+  // RoPE epilogue
+  const uint16_t* rope_cos = nullptr;  // [seq_len][head_dim/2] fp16
+  const uint16_t* rope_sin = nullptr;
+  int seq_len = 0;
+  int rope_cols = 0;                   // columns [0, rope_cols) are rotated
+};
+
+// split_x: activations are f32 and enter the MFMA as an exact fp16 hi + lo
+// pair (two products per block), so the GEMM sees f32 inputs as the WASM
+// path does. Otherwise x is fp16.
+void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
+               const char* prof_name);
+
+// GatherBlockQuantized embedding: out fp16 [T][D].
+void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
+                  uint16_t* out, int T, int V, int D);
+
+// RMSNorm family.
+void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* out, int T, int D, float eps);
+void rms_norm_f32(pfhip_backend* b, const uint16_t* x, const uint16_t* g, float* out, int T, int D, float eps);
+void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
+                      float* norm_out, int T, int D, float eps);
+
+// Element-wise.
+void add_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, uint16_t* out, size_t n);
+void cast_f16_f32(pfhip_backend* b, const uint16_t* src, float* dst, size_t n);
+void cast_f32_f16_scaled(pfhip_backend* b, const float* src, uint16_t* dst, size_t n, float scale);
+void zero_f32(pfhip_backend* b, float* p, size_t n);
+void swiglu_f32(pfhip_backend* b, const float* gu, float* out, int rows, int dff);
+void rope_apply(pfhip_backend* b, uint16_t* qk, const uint16_t* c, const uint16_t* s, int T, int H, int hd,
+                int row_stride, int seq_len);
+
+// Routing.
+void router_topk(pfhip_backend* b, const float* logits, int32_t* idx, float* w, int T, int E, int K,
+                 float weight_scale);
+struct MoePlan {
+  int32_t* counts;      // [nblk][E]
+  int32_t* blk_off;     // [nblk][E]
+  int32_t* expert_off;  // [E+1]
+  int32_t* slot_token;  // [T*K]  token of each expert-sorted slot
+  int32_t* slot_of;     // [T*K]  slot of (token, k)
+  int32_t* tiles;       // [max_tiles][4]
+  int32_t* num_tiles;   // [1]
+  int max_tiles;
+  int tile_t;
+};
+int moe_max_tiles(int T, int K, int E, int tile_t);
+size_t moe_plan_bytes(int T, int K, int E, int tile_t);
+MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t);
+void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const MoePlan& plan);
+void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
+                 const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D);
+void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
+                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, float* norm_out, int T, int K,
+                      int D, float eps);
+void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
+                 int D, int E);
+
+// Banded GQA attention with sinks.
+struct AttnArgs {
+  const uint16_t* q; int q_stride;
+  const uint16_t* k; int k_stride;
+  const uint16_t* v; int v_stride;
+  const float* sinks;   // [Hq] or NULL (no sink = -inf)
+  const uint8_t* mask;  // [B*T] or NULL
+  uint16_t* out; int out_stride;
+  int B, T, Hq, Hkv, head_dim, window;
+  float scale;
+};
+void banded_attention(pfhip_backend* b, const AttnArgs& a);
+
+// Reference-layout kernels kept for the named-dispatch surface.
+void qmoe_gate_up_ref(pfhip_backend* b, const float* x, const int32_t* ridx, const uint8_t* w, const uint16_t* ws,
+                      const uint8_t* wz, const uint16_t* bias, float* out, int T, int K, int N, int D);
+void qmoe_down_scatter_ref(pfhip_backend* b, const float* glu, const int32_t* ridx, const float* rw,
+                           const uint8_t* w, const uint16_t* ws, const uint8_t* wz, const uint16_t* bias, float* acc,
+                           int T, int K, int N, int D);
+
+// Layout probe for the MFMA operand assumption (tests only).
+void probe_mfma_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bm, float* d);
+
+}  // namespace pf

@@ -1,0 +1,651 @@
+// runtime.cpp — the C ABI's device, buffer, encoder and named-dispatch
+// surface (include/pfhip.h). Mirrors the reference's Vulkan bridge verbs
+// (packages/textsift/src/native/vulkan/bridge.h:33-97) on HIP: one stream per
+// backend, device buffers from hipMalloc, an "encoder" that is simply the
+// stream's queue of launches, and a kernel table keyed by name whose entries
+// validate binding counts and push-block sizes before launching
+// (native/vulkan_backend.zig:246-248, 288-290).
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <mutex>
+
+#include "pfhip_internal.h"
+
+namespace pf {
+
+void set_err(char* err, size_t cap, const std::string& msg) {
+  if (!err || cap == 0) return;
+  const size_t n = msg.size() < cap - 1 ? msg.size() : cap - 1;
+  memcpy(err, msg.data(), n);
+  err[n] = 0;
+}
+
+ProfScope::ProfScope(pfhip_backend* b_, const char* n) : b(b_), name(n) {
+  if (b && b->profiling) {
+    if (b->event_pool.size() >= 2) {
+      start = b->event_pool.back();
+      b->event_pool.pop_back();
+      stop = b->event_pool.back();
+      b->event_pool.pop_back();
+    } else {
+      PF_HIP(hipEventCreate(&start));
+      PF_HIP(hipEventCreate(&stop));
+    }
+    PF_HIP(hipEventRecord(start, b->stream));
+  }
+}
+
+ProfScope::~ProfScope() noexcept(false) {
+  if (start) {
+    hipEventRecord(stop, b->stream);
+    b->pending.push_back(ProfPending{name, start, stop});
+  }
+}
+
+void prof_flush(pfhip_backend* b) {
+  if (b->pending.empty()) return;
+  PF_HIP(hipStreamSynchronize(b->stream));
+  for (auto& p : b->pending) {
+    float ms = 0.0f;
+    PF_HIP(hipEventElapsedTime(&ms, p.start, p.stop));
+    auto& e = b->prof[p.name];
+    e.first += 1;
+    e.second += ms;
+    b->event_pool.push_back(p.start);
+    b->event_pool.push_back(p.stop);
+  }
+  b->pending.clear();
+}
+
+// ---------------------------------------------------------------- scratch
+
+struct Scratch {
+  void* ptr = nullptr;
+  size_t size = 0;
+};
+static std::map<pfhip_backend*, Scratch> g_scratch;
+static std::mutex g_scratch_mu;
+
+static void* backend_scratch(pfhip_backend* b, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  Scratch& s = g_scratch[b];
+  if (s.size < bytes) {
+    if (s.ptr) {
+      PF_HIP(hipStreamSynchronize(b->stream));
+      PF_HIP(hipFree(s.ptr));
+      s.ptr = nullptr;
+      s.size = 0;
+    }
+    PF_HIP(hipMalloc(&s.ptr, bytes));
+    s.size = bytes;
+  }
+  return s.ptr;
+}
+
+static void release_scratch(pfhip_backend* b) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(b);
+  if (it != g_scratch.end()) {
+    if (it->second.ptr) hipFree(it->second.ptr);
+    g_scratch.erase(it);
+  }
+}
+
+// ---------------------------------------------------------------- named kernels
+
+struct KernelEntry {
+  const char* name;
+  uint32_t n_bindings;
+  size_t push_bytes;
+  std::function<void(pfhip_backend*, pfhip_buffer* const*, const uint8_t*)> run;
+};
+
+template <class T>
+static T* bp(pfhip_buffer* const* bs, int i) {
+  return static_cast<T*>(bs[i]->ptr);
+}
+static uint32_t pu(const uint8_t* push, int i) {
+  uint32_t v;
+  memcpy(&v, push + 4 * i, 4);
+  return v;
+}
+static float pfv(const uint8_t* push, int i) {
+  float v;
+  memcpy(&v, push + 4 * i, 4);
+  return v;
+}
+static void need(pfhip_buffer* const* bs, int i, size_t bytes, const char* what) {
+  if (bs[i]->size < bytes)
+    throw Error(std::string(what) + ": binding " + std::to_string(i) + " holds " + std::to_string(bs[i]->size) +
+                " bytes, needs " + std::to_string(bytes));
+}
+
+static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* push, bool x_f32, bool out_f32,
+                       const char* name) {
+  const int T = (int)pu(push, 0), N = (int)pu(push, 1), K = (int)pu(push, 2);
+  PF_CHECK(K % 32 == 0, std::string(name) + ": K must be a multiple of 32");
+  const int nb = K / 32;
+  need(bs, 0, (size_t)T * K * (x_f32 ? 4 : 2), name);
+  need(bs, 1, (size_t)N * K / 2, name);
+  need(bs, 2, (size_t)N * nb * 2, name);
+  need(bs, 3, (size_t)N * ((nb + 1) / 2), name);
+  need(bs, 4, (size_t)N * 2, name);
+  need(bs, 5, (size_t)T * N * (out_f32 ? 4 : 2), name);
+  GemmArgs a;
+  a.x = bs[0]->ptr;
+  a.ldx = K;
+  a.w = bp<uint8_t>(bs, 1);
+  a.ws = bp<uint16_t>(bs, 2);
+  a.wz = bp<uint8_t>(bs, 3);
+  a.bias = bp<uint16_t>(bs, 4);
+  a.out = bs[5]->ptr;
+  a.ldo = N;
+  a.M = T;
+  a.N = N;
+  a.K = K;
+  gemm_int4(b, a, x_f32 ? XKind::F32 : XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, T >= 2048 ? 128 : 64, name);
+}
+
+static std::vector<KernelEntry>& registry() {
+  static std::vector<KernelEntry> r;
+  if (!r.empty()) return r;
+  // ---- the reference's 15 kernels (native/vulkan_backend.zig:51-112), WGSL binding order and Dims layout
+  r.push_back({"rms_norm", 3, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), D = (int)pu(p, 1);
+                 need(bs, 0, (size_t)T * D * 2, "rms_norm");
+                 need(bs, 1, (size_t)D * 2, "rms_norm");
+                 need(bs, 2, (size_t)T * D * 2, "rms_norm");
+                 rms_norm_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), T, D, pfv(p, 2));
+               }});
+  r.push_back({"zero_f32", 1, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 need(bs, 0, (size_t)pu(p, 0) * 4, "zero_f32");
+                 zero_f32(b, bp<float>(bs, 0), pu(p, 0));
+               }});
+  r.push_back({"cast_fp16_to_f32", 2, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 need(bs, 0, (size_t)pu(p, 0) * 2, "cast_fp16_to_f32");
+                 need(bs, 1, (size_t)pu(p, 0) * 4, "cast_fp16_to_f32");
+                 cast_f16_f32(b, bp<uint16_t>(bs, 0), bp<float>(bs, 1), pu(p, 0));
+               }});
+  r.push_back({"cast_f32_to_fp16_scaled", 2, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 need(bs, 0, (size_t)pu(p, 0) * 4, "cast_f32_to_fp16_scaled");
+                 need(bs, 1, (size_t)pu(p, 0) * 2, "cast_f32_to_fp16_scaled");
+                 cast_f32_f16_scaled(b, bp<float>(bs, 0), bp<uint16_t>(bs, 1), pu(p, 0), pfv(p, 4));
+               }});
+  r.push_back({"add_fp16", 3, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const size_t n = pu(p, 0);
+                 need(bs, 0, n * 2, "add_fp16");
+                 need(bs, 1, n * 2, "add_fp16");
+                 need(bs, 2, n * 2, "add_fp16");
+                 add_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), n);
+               }});
+  r.push_back({"add_rmsnorm_fp16_to_f32", 5, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), D = (int)pu(p, 1);
+                 for (int i : {0, 1, 3}) need(bs, i, (size_t)T * D * 2, "add_rmsnorm_fp16_to_f32");
+                 need(bs, 2, (size_t)D * 2, "add_rmsnorm_fp16_to_f32");
+                 need(bs, 4, (size_t)T * D * 4, "add_rmsnorm_fp16_to_f32");
+                 add_rms_norm_f32(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2),
+                                  bp<uint16_t>(bs, 3), bp<float>(bs, 4), T, D, pfv(p, 2));
+               }});
+  r.push_back({"embed_lookup_int4", 5, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), V = (int)pu(p, 1), D = (int)pu(p, 2);
+                 const int nb = D / 32;
+                 need(bs, 0, (size_t)V * D / 2, "embed_lookup_int4");
+                 need(bs, 1, (size_t)V * nb * 2, "embed_lookup_int4");
+                 need(bs, 2, (size_t)V * ((nb + 1) / 2), "embed_lookup_int4");
+                 need(bs, 3, (size_t)T * 4, "embed_lookup_int4");
+                 need(bs, 4, (size_t)T * D * 2, "embed_lookup_int4");
+                 embed_lookup(b, bp<uint8_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint8_t>(bs, 2), bp<int32_t>(bs, 3),
+                              bp<uint16_t>(bs, 4), T, V, D);
+               }});
+  r.push_back({"matmul_int4_fp16_f16", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 run_matmul(b, bs, p, false, false, "matmul_int4_fp16_f16");
+               }});
+  r.push_back({"matmul_int4_f32_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 run_matmul(b, bs, p, true, true, "matmul_int4_f32_f32");
+               }});
+  r.push_back({"rope_apply", 3, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), H = (int)pu(p, 1), hd = (int)pu(p, 2);
+                 need(bs, 0, (size_t)T * H * hd * 2, "rope_apply");
+                 need(bs, 1, (size_t)T * (hd / 2) * 2, "rope_apply");
+                 need(bs, 2, (size_t)T * (hd / 2) * 2, "rope_apply");
+                 rope_apply(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), T, H, hd, H * hd, T);
+               }});
+  r.push_back({"banded_attention", 6, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 AttnArgs a{};
+                 a.T = (int)pu(p, 0);
+                 a.Hq = (int)pu(p, 1);
+                 a.Hkv = (int)pu(p, 2);
+                 a.head_dim = (int)pu(p, 3);
+                 a.window = (int)pu(p, 4);
+                 const bool use_mask = pu(p, 5) == 1;
+                 // _pad0 carries an optional f32 score scale; 0 means the
+                 // reference's unscaled Q.K (attention.ts:139-145).
+                 const float sc = pfv(p, 6);
+                 a.scale = sc == 0.0f ? 1.0f : sc;
+                 a.B = 1;
+                 need(bs, 0, (size_t)a.T * a.Hq * a.head_dim * 2, "banded_attention");
+                 need(bs, 1, (size_t)a.T * a.Hkv * a.head_dim * 2, "banded_attention");
+                 need(bs, 2, (size_t)a.T * a.Hkv * a.head_dim * 2, "banded_attention");
+                 need(bs, 3, (size_t)a.Hq * 4, "banded_attention");
+                 if (use_mask) need(bs, 4, (size_t)a.T, "banded_attention");
+                 need(bs, 5, (size_t)a.T * a.Hq * a.head_dim * 2, "banded_attention");
+                 a.q = bp<uint16_t>(bs, 0);
+                 a.q_stride = a.Hq * a.head_dim;
+                 a.k = bp<uint16_t>(bs, 1);
+                 a.k_stride = a.Hkv * a.head_dim;
+                 a.v = bp<uint16_t>(bs, 2);
+                 a.v_stride = a.Hkv * a.head_dim;
+                 a.sinks = bp<float>(bs, 3);
+                 a.mask = use_mask ? bp<uint8_t>(bs, 4) : nullptr;
+                 a.out = bp<uint16_t>(bs, 5);
+                 a.out_stride = a.Hq * a.head_dim;
+                 banded_attention(b, a);
+               }});
+  r.push_back({"router_topk", 3, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), E = (int)pu(p, 1), K = (int)pu(p, 2);
+                 need(bs, 0, (size_t)T * E * 4, "router_topk");
+                 need(bs, 1, (size_t)T * K * 4, "router_topk");
+                 need(bs, 2, (size_t)T * K * 4, "router_topk");
+                 // WASM order (sorted, ties -> lower id) and the 1/K factor of block.ts:99-101
+                 router_topk(b, bp<float>(bs, 0), bp<int32_t>(bs, 1), bp<float>(bs, 2), T, E, K, 1.0f / (float)K);
+               }});
+  r.push_back({"qmoe_gate_up", 7, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), K = (int)pu(p, 1), N = (int)pu(p, 2), D = (int)pu(p, 3);
+                 need(bs, 0, (size_t)T * D * 4, "qmoe_gate_up");
+                 need(bs, 1, (size_t)T * K * 4, "qmoe_gate_up");
+                 need(bs, 6, (size_t)T * K * N * 4, "qmoe_gate_up");
+                 qmoe_gate_up_ref(b, bp<float>(bs, 0), bp<int32_t>(bs, 1), bp<uint8_t>(bs, 2), bp<uint16_t>(bs, 3),
+                                  bp<uint8_t>(bs, 4), bp<uint16_t>(bs, 5), bp<float>(bs, 6), T, K, N, D);
+               }});
+  r.push_back({"swiglu_clamp", 2, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int rows = (int)pu(p, 0), dff = (int)pu(p, 1);
+                 need(bs, 0, (size_t)rows * dff * 8, "swiglu_clamp");
+                 need(bs, 1, (size_t)rows * dff * 4, "swiglu_clamp");
+                 swiglu_f32(b, bp<float>(bs, 0), bp<float>(bs, 1), rows, dff);
+               }});
+  r.push_back({"qmoe_down_scatter", 8, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), K = (int)pu(p, 1), N = (int)pu(p, 2), D = (int)pu(p, 3);
+                 need(bs, 0, (size_t)T * K * D * 4, "qmoe_down_scatter");
+                 need(bs, 7, (size_t)T * N * 4, "qmoe_down_scatter");
+                 qmoe_down_scatter_ref(b, bp<float>(bs, 0), bp<int32_t>(bs, 1), bp<float>(bs, 2), bp<uint8_t>(bs, 3),
+                                       bp<uint16_t>(bs, 4), bp<uint8_t>(bs, 5), bp<uint16_t>(bs, 6), bp<float>(bs, 7),
+                                       T, K, N, D);
+               }});
+  // ---- kernels of this backend
+  r.push_back({"gather_block_quantized", 5, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 for (auto& e : registry())
+                   if (!strcmp(e.name, "embed_lookup_int4")) e.run(b, bs, p);
+               }});
+  r.push_back({"matmul_int4_f32_f16", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 run_matmul(b, bs, p, true, false, "matmul_int4_f32_f16");
+               }});
+  r.push_back({"matmul_int4_fp16_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 run_matmul(b, bs, p, false, true, "matmul_int4_fp16_f32");
+               }});
+  // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
+  r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), K = (int)pu(p, 1), E = (int)pu(p, 2), tt = (int)pu(p, 3);
+                 PF_CHECK(tt == 64 || tt == 128, "moe_route: tile_t must be 64 or 128");
+                 need(bs, 0, (size_t)T * K * 4, "moe_route");
+                 need(bs, 1, (size_t)(E + 1) * 4, "moe_route");
+                 need(bs, 2, (size_t)T * K * 4, "moe_route");
+                 need(bs, 3, (size_t)T * K * 4, "moe_route");
+                 need(bs, 4, (size_t)moe_max_tiles(T, K, E, tt) * 16, "moe_route");
+                 need(bs, 5, 4, "moe_route");
+                 MoePlan m = moe_plan_carve(backend_scratch(b, moe_plan_bytes(T, K, E, tt)), T, K, E, tt);
+                 m.expert_off = bp<int32_t>(bs, 1);
+                 m.slot_token = bp<int32_t>(bs, 2);
+                 m.slot_of = bp<int32_t>(bs, 3);
+                 m.tiles = bp<int32_t>(bs, 4);
+                 m.num_tiles = bp<int32_t>(bs, 5);
+                 moe_route(b, bp<int32_t>(bs, 0), T, K, E, m);
+               }});
+  // moe_ffn: one MoE FFN layer.
+  // push {T, D, E, K, dff, router_int4 (0: fp16 router W [D][E]; 1: MatMulNBits router), x_f32, 0}
+  // bindings [x, router_w, router_scales|-, router_zp|-, router_bias, gu.int4, gu.scales, gu.zp, gu.bias,
+  //           dn.int4, dn.scales, dn.zp, dn.bias, out fp16 [T][D], routing_idx [T][K], routing_w [T][K]]
+  r.push_back({"moe_ffn", 16, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), D = (int)pu(p, 1), E = (int)pu(p, 2), K = (int)pu(p, 3);
+                 const int F = (int)pu(p, 4);
+                 const bool rint4 = pu(p, 5) != 0, xf32 = pu(p, 6) != 0;
+                 PF_CHECK(D % 32 == 0 && F % 32 == 0, "moe_ffn: D and dff must be multiples of 32");
+                 need(bs, 0, (size_t)T * D * (xf32 ? 4 : 2), "moe_ffn");
+                 need(bs, 13, (size_t)T * D * 2, "moe_ffn");
+                 need(bs, 14, (size_t)T * K * 4, "moe_ffn");
+                 need(bs, 15, (size_t)T * K * 4, "moe_ffn");
+                 need(bs, 5, (size_t)E * 2 * F * D / 2, "moe_ffn");
+                 need(bs, 9, (size_t)E * D * F / 2, "moe_ffn");
+                 const int tt = (T * K / E >= 256) ? 128 : 64;
+                 const size_t S = (size_t)T * K;
+                 auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+                 const size_t plan_b = moe_plan_bytes(T, K, E, tt);
+                 const size_t bytes = al((size_t)T * E * 4) + al(S * F * 4) + al(S * D * 4) + al((size_t)T * D * 4) +
+                                      al((size_t)T * D * 2) + plan_b;
+                 char* s = static_cast<char*>(backend_scratch(b, bytes));
+                 float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
+                 float* glu = reinterpret_cast<float*>(s); s += al(S * F * 4);
+                 float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
+                 float* xf = reinterpret_cast<float*>(s); s += al((size_t)T * D * 4);
+                 uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
+                 MoePlan m = moe_plan_carve(s, T, K, E, tt);
+                 // router logits
+                 if (rint4) {
+                   GemmArgs a;
+                   a.x = bs[0]->ptr; a.ldx = D;
+                   a.w = bp<uint8_t>(bs, 1); a.ws = bp<uint16_t>(bs, 2); a.wz = bp<uint8_t>(bs, 3);
+                   a.bias = bp<uint16_t>(bs, 4);
+                   a.out = logits; a.ldo = E; a.M = T; a.N = E; a.K = D;
+                   gemm_int4(b, a, xf32 ? XKind::F32 : XKind::F16, Epi::F32, false, 64, "router_gemm");
+                 } else {
+                   PF_CHECK(!xf32, "moe_ffn: the fp16-weight router takes fp16 activations");
+                   need(bs, 1, (size_t)D * E * 2, "moe_ffn");
+                   router_f16w(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 4), logits, T, D, E);
+                 }
+                 router_topk(b, logits, bp<int32_t>(bs, 14), bp<float>(bs, 15), T, E, K, 1.0f);
+                 moe_route(b, bp<int32_t>(bs, 14), T, K, E, m);
+                 // experts read f32 activations (expert.ts:181-204): widen fp16 input once
+                 const float* xin = static_cast<const float*>(bs[0]->ptr);
+                 if (!xf32) {
+                   cast_f16_f32(b, bp<uint16_t>(bs, 0), xf, (size_t)T * D);
+                   xin = xf;
+                 }
+                 GemmArgs g;
+                 g.x = xin; g.ldx = D; g.row_map = m.slot_token;
+                 g.w = bp<uint8_t>(bs, 5); g.ws = bp<uint16_t>(bs, 6); g.wz = bp<uint8_t>(bs, 7);
+                 g.bias = bp<uint16_t>(bs, 8);
+                 g.w_gs = (size_t)2 * F * D / 2; g.ws_gs = (size_t)2 * F * (D / 32);
+                 g.wz_gs = (size_t)2 * F * ((D / 32 + 1) / 2); g.bias_gs = (size_t)2 * F;
+                 g.out = glu; g.ldo = F; g.M = (int)S; g.N = 2 * F; g.K = D;
+                 g.tiles = m.tiles; g.num_tiles = m.num_tiles; g.max_tiles = m.max_tiles;
+                 gemm_int4(b, g, XKind::F32, Epi::SWIGLU_F32, true, tt, "moe_gate_up");
+                 GemmArgs d;
+                 d.x = glu; d.ldx = F;
+                 d.w = bp<uint8_t>(bs, 9); d.ws = bp<uint16_t>(bs, 10); d.wz = bp<uint8_t>(bs, 11);
+                 d.bias = bp<uint16_t>(bs, 12);
+                 d.w_gs = (size_t)D * F / 2; d.ws_gs = (size_t)D * (F / 32);
+                 d.wz_gs = (size_t)D * ((F / 32 + 1) / 2); d.bias_gs = (size_t)D;
+                 d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
+                 d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
+                 gemm_int4(b, d, XKind::F32, Epi::F32, true, tt, "moe_down");
+                 // out = fp16(sum_k w_k y_k) (zero residual -> h_out holds the MoE output)
+                 zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
+                 moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, zero_res, nullptr,
+                             bp<uint16_t>(bs, 13), T, K, D);
+               }});
+  r.push_back({"probe_mfma_f16", 3, 0, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*) {
+                 need(bs, 0, 16 * 32 * 2, "probe_mfma_f16");
+                 need(bs, 1, 32 * 16 * 2, "probe_mfma_f16");
+                 need(bs, 2, 16 * 16 * 4, "probe_mfma_f16");
+                 probe_mfma_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<float>(bs, 2));
+               }});
+  return r;
+}
+
+static const KernelEntry& find_kernel(const char* name) {
+  for (auto& e : registry())
+    if (!strcmp(e.name, name)) return e;
+  throw Error(std::string("unknown kernel \"") + (name ? name : "(null)") + "\"");
+}
+
+static void run_named(pfhip_backend* b, const char* name, pfhip_buffer* const* bindings, uint32_t n,
+                      const void* push, size_t push_len) {
+  const KernelEntry& k = find_kernel(name);
+  PF_CHECK(n == k.n_bindings, std::string(name) + ": expected " + std::to_string(k.n_bindings) + " bindings, got " +
+                                  std::to_string(n));
+  PF_CHECK(push_len == k.push_bytes, std::string(name) + ": push block must be " + std::to_string(k.push_bytes) +
+                                         " bytes, got " + std::to_string(push_len));
+  for (uint32_t i = 0; i < n; ++i) {
+    PF_CHECK(bindings[i] && bindings[i]->ptr, std::string(name) + ": null binding " + std::to_string(i));
+    PF_CHECK(bindings[i]->owner == b, std::string(name) + ": binding " + std::to_string(i) + " is another backend's");
+  }
+  uint8_t pbuf[64] = {0};
+  if (push_len) memcpy(pbuf, push, push_len);
+  k.run(b, bindings, pbuf);
+}
+
+}  // namespace pf
+
+using namespace pf;
+
+#define PF_TRY(err, cap, body, failret) \
+  try {                                 \
+    body                                \
+  } catch (const std::exception& ex) {  \
+    set_err(err, cap, ex.what());       \
+    return failret;                     \
+  }
+
+extern "C" {
+
+const char* pfhip_version(void) { return "textsift-amd pfhip 0.1 (gfx950)"; }
+
+pfhip_backend* pfhip_create_backend(int device, char* err, size_t cap) {
+  pfhip_backend* b = nullptr;
+  try {
+    int n = 0;
+    PF_HIP(hipGetDeviceCount(&n));
+    PF_CHECK(n > 0, "no HIP device visible");
+    PF_CHECK(device >= 0 && device < n, "device ordinal out of range");
+    hipDeviceProp_t prop;
+    PF_HIP(hipGetDeviceProperties(&prop, device));
+    PF_CHECK(std::string(prop.gcnArchName).rfind("gfx950", 0) == 0,
+             std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only");
+    PF_HIP(hipSetDevice(device));
+    b = new pfhip_backend();
+    b->device = device;
+    b->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    PF_HIP(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
+    return b;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    if (b) {
+      if (b->stream) hipStreamDestroy(b->stream);
+      delete b;
+    }
+    return nullptr;
+  }
+}
+
+void pfhip_destroy_backend(pfhip_backend* b) {
+  if (!b) return;
+  hipSetDevice(b->device);
+  hipStreamSynchronize(b->stream);
+  for (auto& p : b->pending) {
+    hipEventDestroy(p.start);
+    hipEventDestroy(p.stop);
+  }
+  for (auto e : b->event_pool) hipEventDestroy(e);
+  release_scratch(b);
+  hipStreamDestroy(b->stream);
+  delete b;
+}
+
+int pfhip_device_name(pfhip_backend* b, char* out, size_t cap) {
+  if (!b) return -1;
+  set_err(out, cap, b->device_name);
+  return 0;
+}
+
+pfhip_buffer* pfhip_create_buffer(pfhip_backend* b, const void* bytes, size_t n, char* err, size_t cap) {
+  pfhip_buffer* buf = nullptr;
+  try {
+    PF_CHECK(b, "null backend");
+    PF_CHECK(n > 0, "zero-sized buffer");
+    buf = new pfhip_buffer();
+    buf->owner = b;
+    buf->size = n;
+    PF_HIP(hipSetDevice(b->device));
+    PF_HIP(hipMalloc(&buf->ptr, n));
+    if (bytes) {
+      PF_HIP(hipMemcpyAsync(buf->ptr, bytes, n, hipMemcpyHostToDevice, b->stream));
+    } else {
+      PF_HIP(hipMemsetAsync(buf->ptr, 0, n, b->stream));
+    }
+    PF_HIP(hipStreamSynchronize(b->stream));
+    return buf;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    if (buf) {
+      if (buf->ptr) hipFree(buf->ptr);
+      delete buf;
+    }
+    return nullptr;
+  }
+}
+
+pfhip_buffer* pfhip_create_empty_buffer(pfhip_backend* b, size_t n, char* err, size_t cap) {
+  return pfhip_create_buffer(b, nullptr, n, err, cap);
+}
+
+void pfhip_release_buffer(pfhip_backend* b, pfhip_buffer* buf) {
+  if (!buf) return;
+  if (b) hipStreamSynchronize(b->stream);
+  if (buf->ptr) hipFree(buf->ptr);
+  delete buf;
+}
+
+size_t pfhip_buffer_size(const pfhip_buffer* buf) { return buf ? buf->size : 0; }
+void* pfhip_buffer_device_ptr(const pfhip_buffer* buf) { return buf ? buf->ptr : nullptr; }
+
+int pfhip_write_buffer(pfhip_backend* b, pfhip_buffer* buf, size_t off, const void* bytes, size_t n, char* err,
+                       size_t cap) {
+  PF_TRY(err, cap,
+         {
+           PF_CHECK(b && buf && (bytes || n == 0), "null argument");
+           PF_CHECK(off <= buf->size && n <= buf->size - off, "write out of bounds");
+           if (n) {
+             PF_HIP(hipMemcpyAsync(static_cast<char*>(buf->ptr) + off, bytes, n, hipMemcpyHostToDevice, b->stream));
+             PF_HIP(hipStreamSynchronize(b->stream));
+           }
+           return 0;
+         },
+         -1)
+}
+
+int pfhip_read_buffer(pfhip_backend* b, pfhip_buffer* buf, size_t off, void* out, size_t n, char* err, size_t cap) {
+  PF_TRY(err, cap,
+         {
+           PF_CHECK(b && buf && (out || n == 0), "null argument");
+           PF_CHECK(off <= buf->size && n <= buf->size - off, "read out of bounds");
+           if (n) {
+             PF_HIP(hipMemcpyAsync(out, static_cast<char*>(buf->ptr) + off, n, hipMemcpyDeviceToHost, b->stream));
+             PF_HIP(hipStreamSynchronize(b->stream));
+           }
+           prof_flush(b);
+           return 0;
+         },
+         -1)
+}
+
+int pfhip_dispatch_one_shot(pfhip_backend* b, const char* name, pfhip_buffer* const* bindings, uint32_t n,
+                            const void* push, size_t push_len, const uint32_t grid[3], char* err, size_t cap) {
+  (void)grid;
+  PF_TRY(err, cap,
+         {
+           PF_CHECK(b, "null backend");
+           PF_CHECK(!b->encoder_open, "an encoder is open on this backend");
+           PF_HIP(hipSetDevice(b->device));
+           run_named(b, name, bindings, n, push, push_len);
+           PF_HIP(hipStreamSynchronize(b->stream));
+           prof_flush(b);
+           return 0;
+         },
+         -1)
+}
+
+pfhip_encoder* pfhip_begin_encoder(pfhip_backend* b, char* err, size_t cap) {
+  PF_TRY(err, cap,
+         {
+           PF_CHECK(b, "null backend");
+           PF_CHECK(!b->encoder_open, "an encoder is already open on this backend");
+           b->encoder_open = true;
+           pfhip_encoder* e = new pfhip_encoder();
+           e->b = b;
+           return e;
+         },
+         nullptr)
+}
+
+int pfhip_enqueue_dispatch(pfhip_encoder* e, const char* name, pfhip_buffer* const* bindings, uint32_t n,
+                           const void* push, size_t push_len, const uint32_t grid[3], char* err, size_t cap) {
+  (void)grid;
+  PF_TRY(err, cap,
+         {
+           PF_CHECK(e && e->b, "null encoder");
+           PF_HIP(hipSetDevice(e->b->device));
+           run_named(e->b, name, bindings, n, push, push_len);
+           e->dispatches++;
+           return 0;
+         },
+         -1)
+}
+
+int pfhip_submit_and_readback(pfhip_encoder* e, pfhip_buffer* out, size_t off, void* dst, size_t n, char* err,
+                              size_t cap) {
+  if (!e) {
+    set_err(err, cap, "null encoder");
+    return -1;
+  }
+  pfhip_backend* b = e->b;
+  b->encoder_open = false;
+  delete e;
+  return pfhip_read_buffer(b, out, off, dst, n, err, cap);
+}
+
+void pfhip_discard_encoder(pfhip_encoder* e) {
+  if (!e) return;
+  e->b->encoder_open = false;
+  hipStreamSynchronize(e->b->stream);
+  delete e;
+}
+
+const char* pfhip_kernel_names(void) {
+  static std::string s;
+  if (s.empty())
+    for (auto& k : registry())
+      s += std::string(k.name) + " " + std::to_string(k.n_bindings) + " " + std::to_string(k.push_bytes) + "\n";
+  return s.c_str();
+}
+
+int pfhip_profile_enable(pfhip_backend* b, int on) {
+  if (!b) return -1;
+  try {
+    prof_flush(b);
+  } catch (...) {
+    return -1;
+  }
+  b->profiling = on != 0;
+  return 0;
+}
+
+int pfhip_profile_reset(pfhip_backend* b) {
+  if (!b) return -1;
+  try {
+    prof_flush(b);
+  } catch (...) {
+    return -1;
+  }
+  b->prof.clear();
+  return 0;
+}
+
+int pfhip_profile_report(pfhip_backend* b, char* out, size_t cap) {
+  if (!b) return -1;
+  try {
+    prof_flush(b);
+  } catch (const std::exception& ex) {
+    set_err(out, cap, ex.what());
+    return -1;
+  }
+  std::string r;
+  char line[256];
+  for (auto& kv : b->prof) {
+    snprintf(line, sizeof line, "%s %ld %.6f\n", kv.first.c_str(), kv.second.first, kv.second.second);
+    r += line;
+  }
+  set_err(out, cap, r);
+  return 0;
+}
+
+}  // extern "C"
