@@ -64,6 +64,32 @@ def test_mfma_16x16x32_f16_layout(be):
 
 # ---------------------------------------------------------------- MatMulNBits
 
+@pytest.mark.parametrize("zp_random", [False, True])
+def test_gemm_reads_exact_dequantized_weights(be, zp_random):
+    """One-hot activations read the dequantised weights back exactly:
+    out[t][n] = q[n][t] - zp[n][t // 32] with unit scales and zero bias.
+    Pins nibble order, zero-point nibble selection and the exact (q - zp)
+    fp16 encoding of every k position of the block."""
+    T, N, K = 128, 256, 128
+    rng = np.random.default_rng(7)
+    q = rng.integers(0, 16, (N, K)).astype(np.uint8)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    scales = np.full((N, K // 32), 0x3C00, np.uint16)
+    if zp_random:
+        zp = rng.integers(0, 256, (N, 2)).astype(np.uint8)
+        z = np.stack([zp[:, 0] & 15, zp[:, 0] >> 4, zp[:, 1] & 15, zp[:, 1] >> 4], 1).astype(np.int32)
+    else:
+        zp = np.full((N, 2), 0x88, np.uint8)
+        z = np.full((N, 4), 8, np.int32)
+    x = np.zeros((T, K), np.float16)
+    x[np.arange(T), np.arange(T) % K] = 1.0
+    out = run(be, "matmul_int4_fp16_f16", [x.view(np.uint16), packed, scales, zp, np.zeros(N, np.uint16)],
+              T * N * 2, u32s(T, N, K, 0)).view(np.float16).astype(np.float32).reshape(T, N)
+    k = np.arange(T) % K
+    expect = (q[:, k].astype(np.int32) - z[:, k // 32]).T.astype(np.float32)
+    assert np.array_equal(out, expect)
+
+
 def test_matmul_fixture_fp16(be, fixture):
     fx = fixture("matmul_int4_fp16_f16")
     ins = [fx.input("x", np.uint16), fx.input("w_int4"), fx.input("w_scales", np.uint16), fx.input("w_zp"),

@@ -38,21 +38,24 @@ constexpr int BN = 128;         // weight rows (output columns) per workgroup
 constexpr int BK = 64;          // K per LDS stage = two quant blocks
 constexpr int LDW = BK + 8;     // padded LDS row (halves)
 
+// (1024 + a, 1024 + b) - (1024 + zp, 1024 + zp) on packed fp16: exact.
+// Scalars only: __builtin_bit_cast applied to an ext-vector element (r.y)
+// is lowered by this clang as a cast of the previously assigned element.
+__device__ __forceinline__ uint32_t sub_zp(uint32_t v, h2_t off) {
+  const h2_t h = __builtin_bit_cast(h2_t, v) - off;
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 // 8 nibbles of one dword -> 8 exact fp16 values (q - zp), natural k order.
 __device__ __forceinline__ u4_t dequant8(uint32_t w, uint32_t zp_pair) {
   const uint32_t lo = w & 0x0F0F0F0Fu;          // k0 k2 k4 k6
   const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // k1 k3 k5 k7
-  u4_t r;
-  r.x = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u;  // 1024+k0, 1024+k1
-  r.y = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u;
-  r.z = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u;
-  r.w = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u;
   const h2_t off = __builtin_bit_cast(h2_t, zp_pair);  // (1024+zp, 1024+zp)
-  r.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.x) - off);
-  r.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.y) - off);
-  r.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.z) - off);
-  r.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, r.w) - off);
-  return r;
+  const uint32_t p0 = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u;  // 1024+k0, 1024+k1
+  const uint32_t p1 = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u;
+  const uint32_t p2 = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u;
+  const uint32_t p3 = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u;
+  return u4_t{sub_zp(p0, off), sub_zp(p1, off), sub_zp(p2, off), sub_zp(p3, off)};
 }
 
 __device__ __forceinline__ int xcd_remap(int bid, int total) {
