@@ -54,6 +54,15 @@ __device__ __forceinline__ float hw_h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// f32 -> exact (hi, lo) fp16 pair: hi = fp16(v), lo = fp16(v - hi); hi + lo
+// carries 22 significant bits of v (the form SPLIT GEMM inputs take).
+__device__ __forceinline__ void split_hilo(float v, uint16_t& hi, uint16_t& lo) {
+  const _Float16 h = (_Float16)v;
+  const _Float16 l = (_Float16)(v - (float)h);
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, l);
+}
+
 // expApproxNonPositiveF32x4 (zig/wasm_exports.zig:812-838), one lane.
 // Accuracy ~2.8e-4 relative; reproduced, not replaced, so GPU softmax and
 // SwiGLU track the reference's values.

@@ -6,15 +6,15 @@
 // with the GPU decomposition of NodeBackend.forward
 // (native/backend.ts:433-704) collapsed into 11 launches per layer:
 //
-//   [layer 0 only] embed -> h ; rms_norm(h, ln_in) -> xn (f32)
+//   [layer 0 only] embed -> h ; rms_norm(h, ln_in) -> xn (f32 as hi/lo fp16 planes)
 //   per layer l:
 //     QKV GEMM  xn -> qkv (fp16, bias, RoPE on q/k in the epilogue)
 //     banded attention qkv -> att (fp16)
 //     O GEMM    att -> o (fp16)
-//     add+rms_norm  h + o -> h2 (fp16), xn (f32)
+//     add+rms_norm  h + o -> h2 (fp16), xn (hi/lo)
 //     router GEMM xn -> logits (f32); top-k/softmax -> (idx, w)
 //     routing plan: count / scan / scatter (stable counting sort by expert)
-//     gate_up grouped GEMM (gathered xn rows) + SwiGLU -> glu (f32)
+//     gate_up grouped GEMM (gathered xn rows) + SwiGLU -> glu (f32 as hi/lo)
 //     down grouped GEMM glu -> y (f32, slot order)
 //     combine: h_next = fp16(h2 + fp16(sum_k w_k y_k)) ; xn = rms_norm(h_next, next ln)
 //   classifier GEMM xn -> fp16 logits -> f32
@@ -174,7 +174,8 @@ void build_rope_tables(const pfhip_model_config& c, int T, std::vector<uint16_t>
 
 struct Scr {
   uint16_t *h0, *h1, *h2, *qkv, *att, *o, *logits16;
-  float *xn, *rlogits, *rw, *glu, *y, *logits;
+  uint16_t *xn_hi, *xn_lo, *glu_hi, *glu_lo;
+  float *rlogits, *rw, *y, *logits;
   int32_t* ridx;
   void* plan;
 };
@@ -198,14 +199,16 @@ size_t scratch_layout(const pfhip_model_config& c, int M, Scr* s, void* base) {
   t.h0 = (uint16_t*)take((size_t)M * D * 2);
   t.h1 = (uint16_t*)take((size_t)M * D * 2);
   t.h2 = (uint16_t*)take((size_t)M * D * 2);
-  t.xn = (float*)take((size_t)M * D * 4);
+  t.xn_hi = (uint16_t*)take((size_t)M * D * 2);
+  t.xn_lo = (uint16_t*)take((size_t)M * D * 2);
   t.qkv = (uint16_t*)take((size_t)M * NQKV * 2);
   t.att = (uint16_t*)take((size_t)M * HQ * 2);
   t.o = (uint16_t*)take((size_t)M * D * 2);
   t.rlogits = (float*)take((size_t)M * E * 4);
   t.ridx = (int32_t*)take(S * 4);
   t.rw = (float*)take(S * 4);
-  t.glu = (float*)take(S * F * 4);
+  t.glu_hi = (uint16_t*)take(S * F * 2);
+  t.glu_lo = (uint16_t*)take(S * F * 2);
   t.y = (float*)take(S * D * 4);
   t.logits16 = (uint16_t*)take((size_t)M * C * 2);
   t.logits = (float*)take((size_t)M * C * 4);
@@ -272,7 +275,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
-  rms_norm_f32(b, s.h0, m->layers[0].ln_in, s.xn, M, D, c.eps);
+  rms_norm_split(b, s.h0, m->layers[0].ln_in, s.xn_hi, s.xn_lo, M, D, c.eps);
   uint16_t* h = s.h0;
   uint16_t* hn = s.h1;
   for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -280,11 +283,11 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     const std::string tag = std::to_string(l);
     {  // QKV (+bias, RoPE)
       GemmArgs a;
-      a.x = s.xn; a.ldx = D;
+      a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
       a.w = L.qkv.q; a.ws = L.qkv.s; a.wz = L.qkv.z; a.bias = L.qkv.bias;
       a.out = s.qkv; a.ldo = NQKV; a.M = M; a.N = NQKV; a.K = D;
       a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
-      gemm_int4(b, a, XKind::F32, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
+      gemm_int4(b, a, XKind::SPLIT, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
     }
     record_tap(m, "qkv." + tag, s.qkv, (size_t)M * NQKV * 2);
     {
@@ -305,14 +308,14 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.out = s.o; a.ldo = D; a.M = M; a.N = D; a.K = Hq * hd;
       gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
     }
-    add_rms_norm_f32(b, h, s.o, L.ln_post, s.h2, s.xn, M, D, c.eps);
+    add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
     record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
     {
       GemmArgs a;
-      a.x = s.xn; a.ldx = D;
+      a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
       a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
       a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
-      gemm_int4(b, a, XKind::F32, Epi::F32, false, 128, "gemm_router");
+      gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
     }
     router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
     record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
@@ -321,35 +324,35 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     moe_route(b, s.ridx, M, K, E, plan);
     {
       GemmArgs g;
-      g.x = s.xn; g.ldx = D; g.row_map = plan.slot_token;
+      g.x = s.xn_hi; g.x_lo = s.xn_lo; g.ldx = D; g.row_map = plan.slot_token;
       g.w = L.gate_up.q; g.ws = L.gate_up.s; g.wz = L.gate_up.z; g.bias = L.gate_up.bias;
       g.w_gs = q_bytes(2 * F, D); g.ws_gs = s_bytes(2 * F, D) / 2; g.wz_gs = z_bytes(2 * F, D);
       g.bias_gs = (size_t)2 * F;
-      g.out = s.glu; g.ldo = F; g.M = M * K; g.N = 2 * F; g.K = D;
+      g.out = s.glu_hi; g.out_lo = s.glu_lo; g.ldo = F; g.M = M * K; g.N = 2 * F; g.K = D;
       g.tiles = plan.tiles; g.num_tiles = plan.num_tiles; g.max_tiles = plan.max_tiles;
-      gemm_int4(b, g, XKind::F32, Epi::SWIGLU_F32, true, tt, "gemm_moe_gate_up");
+      gemm_int4(b, g, XKind::SPLIT, Epi::SWIGLU_SPLIT, true, tt, "gemm_moe_gate_up");
     }
     {
       GemmArgs d;
-      d.x = s.glu; d.ldx = F;
+      d.x = s.glu_hi; d.x_lo = s.glu_lo; d.ldx = F;
       d.w = L.down.q; d.ws = L.down.s; d.wz = L.down.z; d.bias = L.down.bias;
       d.w_gs = q_bytes(D, F); d.ws_gs = s_bytes(D, F) / 2; d.wz_gs = z_bytes(D, F); d.bias_gs = (size_t)D;
       d.out = s.y; d.ldo = D; d.M = M * K; d.N = D; d.K = F;
       d.tiles = plan.tiles; d.num_tiles = plan.num_tiles; d.max_tiles = plan.max_tiles;
-      gemm_int4(b, d, XKind::F32, Epi::F32, true, tt, "gemm_moe_down");
+      gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "gemm_moe_down");
     }
     const uint16_t* gamma_next = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : W<uint16_t>(m, "final_norm");
-    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn, M, K, D, c.eps);
+    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn_hi, s.xn_lo, M, K, D, c.eps);
     record_tap(m, "h." + tag, hn, (size_t)M * D * 2);
     std::swap(h, hn);
   }
   {
     GemmArgs a;
-    a.x = s.xn; a.ldx = D;
+    a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
     QW sc = qw(m, "score");
     a.w = sc.q; a.ws = sc.s; a.wz = sc.z; a.bias = sc.bias;
     a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
-    gemm_int4(b, a, XKind::F32, Epi::F16, false, 128, "gemm_classifier");
+    gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
   }
   record_tap(m, "logits16", s.logits16, (size_t)M * C * 2);
   // wasm.ts:776-796 widens the fp16 logits IEEE-correctly

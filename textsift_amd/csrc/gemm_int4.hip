@@ -71,8 +71,8 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
   constexpr int WN = BN / 2;   // weight rows per wave
   constexpr int TI = WN / 16;  // n sub-tiles per wave
   constexpr int TJ = WT / 16;  // token sub-tiles per wave
-  // X loader geometry
-  constexpr int XCH = SPLIT ? 16 : 8;            // 16-byte chunks per row per stage
+  // X loader geometry: 8 x 16-byte chunks per row per plane per stage
+  constexpr int XCH = 8;
   constexpr int XRP = 256 / XCH;                 // rows per pass
   constexpr int XPASS = BT / XRP;                // passes
 
@@ -131,67 +131,66 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
     }
   }
 
-  // ---- prefetch registers
+  // ---- prefetch registers: raw bytes only. Nothing loaded here is consumed
+  // before store_stage, so the next stage's loads stay in flight across the
+  // current stage's MFMAs (decoding a scale or zero-point here would make the
+  // compiler wait for the load right away).
   u4_t wreg;
-  uint32_t zreg;   // packed (1024+zp) pair
-  float sreg;
-  u4_t xreg[XPASS];
+  uint32_t sraw;   // fp16 scale bits
+  uint32_t zraw;   // zero-point byte (nibble selected in store_stage)
+  bool wvalid;
+  u4_t xreg[NPL][XPASS];
+  const uint16_t* __restrict__ xhi = static_cast<const uint16_t*>(p.x);
+  const uint16_t* __restrict__ xlo = p.x_lo;
+  int kb_cur = 0;
 
   auto load_stage = [&](int s) {
     const int kb = s * 2 + wb;
-    if (w_ok && kb < nb) {
+    kb_cur = kb;
+    wvalid = w_ok && kb < nb;
+    if (wvalid) {
       wreg = *reinterpret_cast<const u4_t*>(wsrc + kb * 16);
-      sreg = wasm_h2f(WS[(size_t)wrow * nb + kb]);
-      uint32_t zp = 0;
-      if (WZ) {
-        const uint8_t zb = WZ[(size_t)wrow * zstride + (kb >> 1)];
-        zp = (kb & 1) ? (zb >> 4) : (zb & 0xF);
-      }
-      const uint32_t hz = 0x6400u + zp;  // fp16 bits of 1024 + zp
-      zreg = hz | (hz << 16);
-    } else {
-      wreg = u4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-      zreg = 0x64086408u;  // (q - 8) with q = 8 -> exact zeros
-      sreg = 0.0f;
+      sraw = WS[(size_t)wrow * nb + kb];
+      zraw = WZ ? (uint32_t)WZ[(size_t)wrow * zstride + (kb >> 1)] : 0u;
     }
 #pragma unroll
     for (int i = 0; i < XPASS; ++i) {
-      const int k = s * BK + xc * (SPLIT ? 4 : 8);
+      const int k = s * BK + xc * 8;
       if (xoff[i] >= 0 && k < K) {
-        if constexpr (SPLIT)
-          xreg[i] = *reinterpret_cast<const u4_t*>(static_cast<const float*>(p.x) + xoff[i] + k);
-        else
-          xreg[i] = *reinterpret_cast<const u4_t*>(static_cast<const uint16_t*>(p.x) + xoff[i] + k);
+        xreg[0][i] = *reinterpret_cast<const u4_t*>(xhi + xoff[i] + k);
+        if constexpr (SPLIT) xreg[1][i] = *reinterpret_cast<const u4_t*>(xlo + xoff[i] + k);
       } else {
-        xreg[i] = u4_t{0u, 0u, 0u, 0u};
+        xreg[0][i] = u4_t{0u, 0u, 0u, 0u};
+        if constexpr (SPLIT) xreg[1][i] = u4_t{0u, 0u, 0u, 0u};
       }
     }
   };
 
   auto store_stage = [&]() {
-    // W: 32 nibbles -> 32 exact fp16 at Wl[wr][wb*32 ...]
+    // W: 32 nibbles -> 32 exact fp16 at Wl[wr][wb*32 ...]; invalid rows /
+    // blocks store q = 8 with zp = 8 (exact zeros) and scale 0.
+    u4_t wq = u4_t{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+    uint32_t zp = 8;
+    float sc = 0.0f;
+    if (wvalid) {
+      wq = wreg;
+      sc = wasm_h2f((uint16_t)sraw);
+      zp = WZ ? ((kb_cur & 1) ? (zraw >> 4) : (zraw & 0xFu)) : 0u;
+    }
+    const uint32_t hz = 0x6400u + zp;  // fp16 bits of 1024 + zp
+    const uint32_t zreg = hz | (hz << 16);
     u4_t* wdst = reinterpret_cast<u4_t*>(&Wl[wr * LDW + wb * 32]);
-    wdst[0] = dequant8(wreg.x, zreg);
-    wdst[1] = dequant8(wreg.y, zreg);
-    wdst[2] = dequant8(wreg.z, zreg);
-    wdst[3] = dequant8(wreg.w, zreg);
-    Sl[wb * BN + wr] = sreg;
+    wdst[0] = dequant8(wq.x, zreg);
+    wdst[1] = dequant8(wq.y, zreg);
+    wdst[2] = dequant8(wq.z, zreg);
+    wdst[3] = dequant8(wq.w, zreg);
+    Sl[wb * BN + wr] = sc;
 #pragma unroll
     for (int i = 0; i < XPASS; ++i) {
       const int r = xr + i * XRP;
-      if constexpr (SPLIT) {
-        const f4_t v = __builtin_bit_cast(f4_t, xreg[i]);
-        h4_t hi, lo;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          hi[c] = (_Float16)v[c];
-          lo[c] = (_Float16)(v[c] - (float)hi[c]);
-        }
-        *reinterpret_cast<h4_t*>(&Xl[r * LDW + xc * 4]) = hi;
-        *reinterpret_cast<h4_t*>(&Xl[BT * LDW + r * LDW + xc * 4]) = lo;
-      } else {
-        *reinterpret_cast<u4_t*>(&Xl[r * LDW + xc * 8]) = xreg[i];
-      }
+      for (int pl = 0; pl < NPL; ++pl)
+        *reinterpret_cast<u4_t*>(&Xl[pl * BT * LDW + r * LDW + xc * 8]) = xreg[pl][i];
     }
   };
 
@@ -293,9 +292,16 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
         const float g0 = swiglu_clamp(v[0], v[1]);
         const float g1 = swiglu_clamp(v[2], v[3]);
         const size_t oc = (size_t)(n >> 1);
-        if constexpr (EPI == Epi::SWIGLU_F32) {
-          float* o = static_cast<float*>(p.out) + orow * p.ldo + oc;
-          *reinterpret_cast<float2*>(o) = make_float2(g0, g1);
+        if constexpr (EPI == Epi::SWIGLU_SPLIT) {
+          // f32 SwiGLU output (expert.ts keeps it f32) as hi/lo fp16 planes
+          const _Float16 h0 = (_Float16)g0, h1 = (_Float16)g1;
+          const _Float16 e0 = (_Float16)(g0 - (float)h0), e1 = (_Float16)(g1 - (float)h1);
+          uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
+          uint16_t* ol = p.out_lo + orow * p.ldo + oc;
+          *reinterpret_cast<uint32_t*>(o) =
+              (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          *reinterpret_cast<uint32_t*>(ol) =
+              (uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
         } else {
           uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
           *reinterpret_cast<uint32_t*>(o) = (uint32_t)wasm_f2h(g0) | ((uint32_t)wasm_f2h(g1) << 16);
@@ -323,7 +329,7 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
     case Epi::F16: return launch<BT, SPLIT, Epi::F16, GROUPED>(b, a, name);
     case Epi::F32: return launch<BT, SPLIT, Epi::F32, GROUPED>(b, a, name);
     case Epi::ROPE_F16: return launch<BT, SPLIT, Epi::ROPE_F16, GROUPED>(b, a, name);
-    case Epi::SWIGLU_F32: return launch<BT, SPLIT, Epi::SWIGLU_F32, GROUPED>(b, a, name);
+    case Epi::SWIGLU_SPLIT: return launch<BT, SPLIT, Epi::SWIGLU_SPLIT, GROUPED>(b, a, name);
     case Epi::SWIGLU_F16: return launch<BT, SPLIT, Epi::SWIGLU_F16, GROUPED>(b, a, name);
   }
 }
@@ -335,18 +341,20 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
   PF_CHECK(a.K > 0 && a.K % 32 == 0, "gemm_int4: K must be a positive multiple of 32");
   PF_CHECK(a.N > 0, "gemm_int4: N must be positive");
   PF_CHECK(a.x && a.w && a.ws && a.out, "gemm_int4: null operand");
-  const int xalign = xk == XKind::F32 ? 4 : 8;  // 16-byte vector loads
-  PF_CHECK(a.ldx % xalign == 0 && a.K % 8 == 0, "gemm_int4: activation row stride must allow 16-byte loads");
+  PF_CHECK(a.ldx % 8 == 0 && a.K % 8 == 0, "gemm_int4: activation row stride must allow 16-byte loads");
   PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
            "gemm_int4: activations and weights must be 16-byte aligned");
+  if (xk == XKind::SPLIT)
+    PF_CHECK(a.x_lo && (reinterpret_cast<uintptr_t>(a.x_lo) & 15) == 0, "gemm_int4: SPLIT needs an aligned lo plane");
   PF_CHECK(a.K / 2 % 16 == 0, "gemm_int4: packed weight rows must be 16-byte multiples");
-  if (epi == Epi::SWIGLU_F32 || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_int4: SwiGLU needs N % 4 == 0");
+  if (epi == Epi::SWIGLU_SPLIT || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_int4: SwiGLU needs N % 4 == 0");
+  if (epi == Epi::SWIGLU_SPLIT) PF_CHECK(a.out_lo, "gemm_int4: SWIGLU_SPLIT needs an output lo plane");
   if (epi == Epi::ROPE_F16)
     PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
              "gemm_int4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_int4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_int4: M must be non-negative");
-  const bool split = xk == XKind::F32;
+  const bool split = xk == XKind::SPLIT;
   if (tile_t == 64) {
     if (split) {
       if (grouped) dispatch_epi<64, true, true>(b, a, epi, prof_name);

@@ -60,9 +60,27 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ q, co
 // (D <= 64 * 16). Widening is the reference's bit trick (wasm_h2f).
 constexpr int MAXPL = 16;  // elements per lane
 
-template <bool OUT_F32>
+// Output forms of a normalised row: fp16, f32, or the f32 value as hi/lo fp16 planes.
+enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_SPLIT = 2 };
+
+template <int MODE>
+__device__ __forceinline__ void put(void* out, uint16_t* out_lo, size_t i, float y) {
+  if constexpr (MODE == OUT_F32) {
+    static_cast<float*>(out)[i] = y;
+  } else if constexpr (MODE == OUT_F16) {
+    static_cast<uint16_t*>(out)[i] = wasm_f2h(y);
+  } else {
+    uint16_t h, l;
+    split_hilo(y, h, l);
+    static_cast<uint16_t*>(out)[i] = h;
+    out_lo[i] = l;
+  }
+}
+
+template <int MODE>
 __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ g,
-                                                  void* __restrict__ out, int T, int D, float eps) {
+                                                  void* __restrict__ out, uint16_t* __restrict__ out_lo, int T, int D,
+                                                  float eps) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -81,20 +99,18 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x
 #pragma unroll
   for (int i = 0; i < MAXPL; ++i) {
     const int d = i * 64 + lane;
-    if (d < D) {
-      const float y = v[i] * inv_rms * wasm_h2f(g[d]);
-      if constexpr (OUT_F32) static_cast<float*>(out)[(size_t)t * D + d] = y;
-      else static_cast<uint16_t*>(out)[(size_t)t * D + d] = wasm_f2h(y);
-    }
+    if (d < D) put<MODE>(out, out_lo, (size_t)t * D + d, v[i] * inv_rms * wasm_h2f(g[d]));
   }
 }
 
 // add_rmsnorm_fp16_to_f32 (:288-350): sum = a + b (fp16 store), sumsq of the
 // unrounded f32 sum, normalise the rounded sum.
+template <int MODE>
 __global__ __launch_bounds__(256) void k_add_rms_norm(const uint16_t* __restrict__ a,
                                                       const uint16_t* __restrict__ bb,
                                                       const uint16_t* __restrict__ g, uint16_t* __restrict__ sum_out,
-                                                      float* __restrict__ norm_out, int T, int D, float eps) {
+                                                      void* __restrict__ norm_out, uint16_t* __restrict__ norm_lo,
+                                                      int T, int D, float eps) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -117,12 +133,16 @@ __global__ __launch_bounds__(256) void k_add_rms_norm(const uint16_t* __restrict
 #pragma unroll
   for (int i = 0; i < MAXPL; ++i) {
     const int d = i * 64 + lane;
-    if (d < D) norm_out[base + d] = wasm_h2f(hs[i]) * inv_rms * wasm_h2f(g[d]);
+    if (d < D) put<MODE>(norm_out, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(g[d]));
   }
 }
 
 // ----------------------------------------------------------------------------
 // Element-wise (:969-1164).
+__global__ void k_split_f32(const float* x, uint16_t* hi, uint16_t* lo, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    split_hilo(x[i], hi[i], lo[i]);
+}
 __global__ void k_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* o, size_t n) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
     o[i] = wasm_f2h(wasm_h2f(a[i]) + wasm_h2f(b[i]));
@@ -326,7 +346,8 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
                                                      const int32_t* __restrict__ slot_of, const float* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
                                                      uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
-                                                     const uint16_t* __restrict__ gamma, float* __restrict__ norm_out,
+                                                     const uint16_t* __restrict__ gamma,
+                                                     uint16_t* __restrict__ norm_hi, uint16_t* __restrict__ norm_lo,
                                                      int T, int K, int D, float eps) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
@@ -369,7 +390,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
 #pragma unroll
     for (int i = 0; i < MAXPL; ++i) {
       const int d = i * 64 + lane;
-      if (d < D) norm_out[base + d] = wasm_h2f(hs[i]) * inv_rms * wasm_h2f(gamma[d]);
+      if (d < D) put<OUT_SPLIT>(norm_hi, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(gamma[d]));
     }
   }
 }
@@ -474,7 +495,7 @@ void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16
   PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm");
-  hipLaunchKernelGGL(k_rms_norm<false>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, T, D, eps);
+  hipLaunchKernelGGL(k_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
   PF_HIP(hipGetLastError());
 }
 
@@ -482,7 +503,16 @@ void rms_norm_f32(pfhip_backend* b, const uint16_t* x, const uint16_t* g, float*
   PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm_fp16_to_f32");
-  hipLaunchKernelGGL(k_rms_norm<true>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, T, D, eps);
+  hipLaunchKernelGGL(k_rms_norm<OUT_F32>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
+  PF_HIP(hipGetLastError());
+}
+
+void rms_norm_split(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* hi, uint16_t* lo, int T, int D,
+                    float eps) {
+  PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
+  if (T <= 0) return;
+  ProfScope ps(b, "rms_norm_split");
+  hipLaunchKernelGGL(k_rms_norm<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, hi, lo, T, D, eps);
   PF_HIP(hipGetLastError());
 }
 
@@ -491,8 +521,25 @@ void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, c
   PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
   if (T <= 0) return;
   ProfScope ps(b, "add_rmsnorm_fp16_to_f32");
-  hipLaunchKernelGGL(k_add_rms_norm, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out, norm_out, T, D,
-                     eps);
+  hipLaunchKernelGGL(k_add_rms_norm<OUT_F32>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out,
+                     norm_out, nullptr, T, D, eps);
+  PF_HIP(hipGetLastError());
+}
+
+void add_rms_norm_split(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g,
+                        uint16_t* sum_out, uint16_t* hi, uint16_t* lo, int T, int D, float eps) {
+  PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
+  if (T <= 0) return;
+  ProfScope ps(b, "add_rmsnorm_split");
+  hipLaunchKernelGGL(k_add_rms_norm<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out, hi,
+                     lo, T, D, eps);
+  PF_HIP(hipGetLastError());
+}
+
+void split_f32(pfhip_backend* b, const float* x, uint16_t* hi, uint16_t* lo, size_t n) {
+  if (!n) return;
+  ProfScope ps(b, "split_f32");
+  hipLaunchKernelGGL(k_split_f32, dim3(grid1d(n)), dim3(256), 0, b->stream, x, hi, lo, n);
   PF_HIP(hipGetLastError());
 }
 
@@ -605,18 +652,18 @@ void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine");
   hipLaunchKernelGGL(k_moe_combine<false>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
-                     moe_out, h_out, nullptr, nullptr, T, K, D, 0.0f);
+                     moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
   PF_HIP(hipGetLastError());
 }
 
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
-                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, float* norm_out, int T, int K,
-                      int D, float eps) {
+                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
+                      uint16_t* norm_lo, int T, int K, int D, float eps) {
   PF_CHECK(D <= 64 * MAXPL && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine_norm");
   hipLaunchKernelGGL(k_moe_combine<true>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
-                     nullptr, h_out, gamma, norm_out, T, K, D, eps);
+                     nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
   PF_HIP(hipGetLastError());
 }
 

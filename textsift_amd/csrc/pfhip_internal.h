@@ -81,11 +81,15 @@ void set_err(char* err, size_t cap, const std::string& msg);
 // b->stream, validates its shapes on the host first and throws pf::Error.
 
 // MatMulNBits int4 GEMM.
-enum class XKind { F16, F32 };
-enum class Epi { F16, F32, ROPE_F16, SWIGLU_F32, SWIGLU_F16 };
+// F16: activations are one fp16 plane. SPLIT: f32 activations carried as two
+// fp16 planes, hi = fp16(v) and lo = fp16(v - hi) (22 significant bits), which
+// enter the MFMA as two products per block into the same partial sum.
+enum class XKind { F16, SPLIT };
+enum class Epi { F16, F32, ROPE_F16, SWIGLU_SPLIT, SWIGLU_F16 };
 
 struct GemmArgs {
-  const void* x = nullptr;       // activations [rows][K] (fp16 or f32)
+  const void* x = nullptr;       // activations [rows][K] fp16 (the hi plane in SPLIT mode)
+  const uint16_t* x_lo = nullptr;  // SPLIT: the lo plane, same row stride
   int ldx = 0;                   // row stride in elements
   const int32_t* row_map = nullptr;  // optional gather: logical row r reads x row row_map[r]
   const uint8_t* w = nullptr;    // [N][K/2] uint4 (per group stride w_gs bytes)
@@ -94,6 +98,7 @@ struct GemmArgs {
   const uint16_t* bias = nullptr;  // [N] fp16, NULL = 0
   size_t w_gs = 0, ws_gs = 0, wz_gs = 0, bias_gs = 0;  // per-expert strides (elements)
   void* out = nullptr;
+  uint16_t* out_lo = nullptr;    // SWIGLU_SPLIT: lo plane of the output
   int ldo = 0;
   int M = 0, N = 0, K = 0;
   // grouped (per-expert) mode
@@ -107,9 +112,6 @@ struct GemmArgs {
   int rope_cols = 0;                   // columns [0, rope_cols) are rotated
 };
 
-// split_x: activations are f32 and enter the MFMA as an exact fp16 hi + lo
-// pair (two products per block), so the GEMM sees f32 inputs as the WASM
-// path does. Otherwise x is fp16.
 void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
                const char* prof_name);
 
@@ -117,11 +119,18 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D);
 
-// RMSNorm family.
+// RMSNorm family. The *_split variants write the f32 result as hi/lo fp16
+// planes (norm_hi, norm_lo) for SPLIT GEMM inputs.
 void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* out, int T, int D, float eps);
 void rms_norm_f32(pfhip_backend* b, const uint16_t* x, const uint16_t* g, float* out, int T, int D, float eps);
+void rms_norm_split(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* hi, uint16_t* lo, int T, int D,
+                    float eps);
 void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
                       float* norm_out, int T, int D, float eps);
+void add_rms_norm_split(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g,
+                        uint16_t* sum_out, uint16_t* hi, uint16_t* lo, int T, int D, float eps);
+// f32 -> (hi, lo) fp16 planes.
+void split_f32(pfhip_backend* b, const float* x, uint16_t* hi, uint16_t* lo, size_t n);
 
 // Element-wise.
 void add_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, uint16_t* out, size_t n);
@@ -153,8 +162,8 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                  const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D);
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
-                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, float* norm_out, int T, int K,
-                      int D, float eps);
+                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
+                      uint16_t* norm_lo, int T, int K, int D, float eps);
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
                  int D, int E);
 

@@ -134,6 +134,14 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
   need(bs, 5, (size_t)T * N * (out_f32 ? 4 : 2), name);
   GemmArgs a;
   a.x = bs[0]->ptr;
+  if (x_f32) {  // f32 activations -> hi/lo fp16 planes in scratch
+    const size_t n = (size_t)T * K;
+    uint16_t* planes = static_cast<uint16_t*>(backend_scratch(b, ((n * 2 + 255) & ~(size_t)255) * 2));
+    uint16_t* lo = planes + (((n * 2 + 255) & ~(size_t)255) / 2);
+    split_f32(b, bp<float>(bs, 0), planes, lo, n);
+    a.x = planes;
+    a.x_lo = lo;
+  }
   a.ldx = K;
   a.w = bp<uint8_t>(bs, 1);
   a.ws = bp<uint16_t>(bs, 2);
@@ -144,7 +152,7 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
   a.M = T;
   a.N = N;
   a.K = K;
-  gemm_int4(b, a, x_f32 ? XKind::F32 : XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, T >= 2048 ? 128 : 64, name);
+  gemm_int4(b, a, x_f32 ? XKind::SPLIT : XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, T >= 2048 ? 128 : 64, name);
 }
 
 static std::vector<KernelEntry>& registry() {
@@ -320,23 +328,32 @@ static std::vector<KernelEntry>& registry() {
                  const size_t S = (size_t)T * K;
                  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
                  const size_t plan_b = moe_plan_bytes(T, K, E, tt);
-                 const size_t bytes = al((size_t)T * E * 4) + al(S * F * 4) + al(S * D * 4) + al((size_t)T * D * 4) +
-                                      al((size_t)T * D * 2) + plan_b;
+                 const size_t bytes = al((size_t)T * E * 4) + 2 * al(S * F * 2) + al(S * D * 4) +
+                                      2 * al((size_t)T * D * 2) + al((size_t)T * D * 2) + plan_b;
                  char* s = static_cast<char*>(backend_scratch(b, bytes));
                  float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
-                 float* glu = reinterpret_cast<float*>(s); s += al(S * F * 4);
+                 uint16_t* glu_hi = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
+                 uint16_t* glu_lo = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
                  float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
-                 float* xf = reinterpret_cast<float*>(s); s += al((size_t)T * D * 4);
+                 uint16_t* x_hi = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
+                 uint16_t* x_lo = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  MoePlan m = moe_plan_carve(s, T, K, E, tt);
+                 // activations: f32 input -> hi/lo planes; an fp16 input is exact as one plane
+                 const XKind xk = xf32 ? XKind::SPLIT : XKind::F16;
+                 const void* xin = bs[0]->ptr;
+                 if (xf32) {
+                   split_f32(b, bp<float>(bs, 0), x_hi, x_lo, (size_t)T * D);
+                   xin = x_hi;
+                 }
                  // router logits
                  if (rint4) {
                    GemmArgs a;
-                   a.x = bs[0]->ptr; a.ldx = D;
+                   a.x = xin; a.x_lo = x_lo; a.ldx = D;
                    a.w = bp<uint8_t>(bs, 1); a.ws = bp<uint16_t>(bs, 2); a.wz = bp<uint8_t>(bs, 3);
                    a.bias = bp<uint16_t>(bs, 4);
                    a.out = logits; a.ldo = E; a.M = T; a.N = E; a.K = D;
-                   gemm_int4(b, a, xf32 ? XKind::F32 : XKind::F16, Epi::F32, false, 64, "router_gemm");
+                   gemm_int4(b, a, xk, Epi::F32, false, 64, "router_gemm");
                  } else {
                    PF_CHECK(!xf32, "moe_ffn: the fp16-weight router takes fp16 activations");
                    need(bs, 1, (size_t)D * E * 2, "moe_ffn");
@@ -344,30 +361,24 @@ static std::vector<KernelEntry>& registry() {
                  }
                  router_topk(b, logits, bp<int32_t>(bs, 14), bp<float>(bs, 15), T, E, K, 1.0f);
                  moe_route(b, bp<int32_t>(bs, 14), T, K, E, m);
-                 // experts read f32 activations (expert.ts:181-204): widen fp16 input once
-                 const float* xin = static_cast<const float*>(bs[0]->ptr);
-                 if (!xf32) {
-                   cast_f16_f32(b, bp<uint16_t>(bs, 0), xf, (size_t)T * D);
-                   xin = xf;
-                 }
                  GemmArgs g;
-                 g.x = xin; g.ldx = D; g.row_map = m.slot_token;
+                 g.x = xin; g.x_lo = x_lo; g.ldx = D; g.row_map = m.slot_token;
                  g.w = bp<uint8_t>(bs, 5); g.ws = bp<uint16_t>(bs, 6); g.wz = bp<uint8_t>(bs, 7);
                  g.bias = bp<uint16_t>(bs, 8);
                  g.w_gs = (size_t)2 * F * D / 2; g.ws_gs = (size_t)2 * F * (D / 32);
                  g.wz_gs = (size_t)2 * F * ((D / 32 + 1) / 2); g.bias_gs = (size_t)2 * F;
-                 g.out = glu; g.ldo = F; g.M = (int)S; g.N = 2 * F; g.K = D;
+                 g.out = glu_hi; g.out_lo = glu_lo; g.ldo = F; g.M = (int)S; g.N = 2 * F; g.K = D;
                  g.tiles = m.tiles; g.num_tiles = m.num_tiles; g.max_tiles = m.max_tiles;
-                 gemm_int4(b, g, XKind::F32, Epi::SWIGLU_F32, true, tt, "moe_gate_up");
+                 gemm_int4(b, g, xk, Epi::SWIGLU_SPLIT, true, tt, "moe_gate_up");
                  GemmArgs d;
-                 d.x = glu; d.ldx = F;
+                 d.x = glu_hi; d.x_lo = glu_lo; d.ldx = F;
                  d.w = bp<uint8_t>(bs, 9); d.ws = bp<uint16_t>(bs, 10); d.wz = bp<uint8_t>(bs, 11);
                  d.bias = bp<uint16_t>(bs, 12);
                  d.w_gs = (size_t)D * F / 2; d.ws_gs = (size_t)D * (F / 32);
                  d.wz_gs = (size_t)D * ((F / 32 + 1) / 2); d.bias_gs = (size_t)D;
                  d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
                  d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
-                 gemm_int4(b, d, XKind::F32, Epi::F32, true, tt, "moe_down");
+                 gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "moe_down");
                  // out = fp16(sum_k w_k y_k) (zero residual -> h_out holds the MoE output)
                  zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
                  moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, zero_res, nullptr,
