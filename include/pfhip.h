@@ -119,7 +119,18 @@ typedef struct {
   double rope_beta_slow;  /* 1 */
   uint32_t rope_orig_max; /* 4096 */
   uint32_t rope_truncate; /* 0 */
+  /* Numerics of the GEMM inputs:
+   * PFHIP_PRECISION_FP16  activations enter the int4 GEMMs as fp16 and the
+   *                       block scale is folded into fp16 weights (what the
+   *                       reference's GPU paths feed their GEMMs);
+   * PFHIP_PRECISION_SPLIT activations keep f32 precision as hi/lo fp16 planes
+   *                       and weights enter as exact (q - zp) with the scale
+   *                       applied per block in f32 (the WASM path's numerics). */
+  uint32_t precision;
 } pfhip_model_config;
+
+#define PFHIP_PRECISION_FP16 0u
+#define PFHIP_PRECISION_SPLIT 1u
 
 pfhip_model* pfhip_model_create(pfhip_backend* b, const pfhip_model_config* cfg, char* err, size_t err_cap);
 void pfhip_model_destroy(pfhip_model* m);

@@ -4,25 +4,27 @@ HipBackend / C ABI, against the oracle forward on identical seeded inputs.
 Bars: logits within rel-err 2e-3 (normwise) and per-token argmax agreement
 >= 99.9 %. Per-layer taps are also compared block by block (oracle block fed
 the GPU's own input residual), which isolates one layer's error from the
-accumulation of the layers before it."""
+accumulation of the layers before it. Every test runs for both GEMM input
+precisions (fp16 with scale-folded weights, and the f32 hi/lo split)."""
 import numpy as np
 import pytest
 
 import oracle
 from parity_util import f16, rel_err_norm
-from textsift_amd import synth
+from textsift_amd import _native, synth
 from textsift_amd.backend import HipBackend
 from textsift_amd.config import PF_CONFIG
 
 pytestmark = pytest.mark.gpu
 
 L, E, V = 2, 16, 4096
+PRECISIONS = [_native.PRECISION_FP16, _native.PRECISION_SPLIT]
 
 
-@pytest.fixture(scope="module")
-def small():
+@pytest.fixture(scope="module", params=PRECISIONS, ids=["fp16", "split"])
+def small(request):
     w = synth.make_model_weights(PF_CONFIG, seed=11, num_layers=L, num_experts=E, vocab_size=V)
-    be = HipBackend(w)
+    be = HipBackend(w, precision=request.param)
     be.warmup()
     be.warmup()  # idempotent (native/backend.ts:408)
     yield w, be
@@ -49,7 +51,9 @@ def test_small_forward_vs_oracle(small, T, masked):
         mask[-20:] = 0
     got = be.forward(ids, mask).as_matrix()
     ref = f16(oracle.model_forward(PF_CONFIG, w, ids, mask=mask, num_layers=L)).astype(np.float32)
-    assert rel_err_norm(got, ref) < 2e-3
+    err = rel_err_norm(got, ref)
+    print(f"small model T={T} masked={masked}: rel-err {err:.3e}")
+    assert err < 2e-3
     assert np.mean(np.argmax(got, 1) == np.argmax(ref, 1)) >= 0.999 or T < 100
 
 
@@ -87,25 +91,35 @@ def test_per_layer_taps_vs_oracle_block(small):
         assert rc == 0
         gpu_h = m.tap(f"h.{l}", np.uint16, T * D).reshape(T, D)
         err = rel_err_norm(f16(gpu_h), f16(out))
+        print(f"layer {l}: rel-err {err:.3e}")
         assert err < 2e-3, f"layer {l}: {err}"
         h_in = gpu_h  # next block starts from the GPU's residual
     m.enable_taps(False)
 
 
-@pytest.mark.parametrize("T", [2048])
-def test_full_model_forward_vs_oracle(T):
+@pytest.fixture(scope="module")
+def full_ref():
+    """Oracle logits of the full-size model for one T=2048 sequence."""
+    T = 2048
+    w = synth.make_model_weights(PF_CONFIG, seed=20260101)
+    ids = synth.token_ids(1000, T)
+    ref = f16(oracle.model_forward(PF_CONFIG, w, ids, n_threads=8)).astype(np.float32)
+    return w, ids, ref
+
+
+@pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
+def test_full_model_forward_vs_oracle(full_ref, precision):
     """BASELINE config 5 architecture at full size (8 layers, 128 experts,
     vocab 200064), one T=2048 sequence (the reference's chunk length)."""
-    w = synth.make_model_weights(PF_CONFIG, seed=20260101)
-    be = HipBackend(w)
+    w, ids, ref = full_ref
+    T = ids.size
+    be = HipBackend(w, precision=precision)
     be.warmup()
     try:
-        ids = synth.token_ids(1000, T)
         got = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
-        ref = f16(oracle.model_forward(PF_CONFIG, w, ids, n_threads=8)).astype(np.float32)
         err = rel_err_norm(got, ref)
         agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
-        print(f"full model T={T}: rel-err {err:.3e}, argmax agreement {agree:.5f}")
+        print(f"full model T={T} precision={precision}: rel-err {err:.3e}, argmax agreement {agree:.5f}")
         assert err < 2e-3
         assert agree >= 0.999
     finally:

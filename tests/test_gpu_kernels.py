@@ -139,6 +139,59 @@ def test_matmul_f32_split_vs_oracle(be, T, N, K):
     assert np.all(np.abs(out - ref) <= bound)
 
 
+def folded_weights(w, N, K):
+    """fp16((q - zp) * scale): the weights gemm_w4 multiplies by (the scale
+    folded into each weight, rounded once to fp16)."""
+    q = np.empty((N, K), np.int32)
+    q[:, 0::2] = w["int4"].reshape(N, K // 2) & 15
+    q[:, 1::2] = w["int4"].reshape(N, K // 2) >> 4
+    nb = K // 32
+    zb = w["zp"].reshape(N, (nb + 1) // 2)
+    zp = np.empty((N, nb), np.int32)
+    zp[:, 0::2] = zb[:, : (nb + 1) // 2] & 15
+    zp[:, 1::2] = zb[:, : nb // 2] >> 4
+    s = w["scales"].reshape(N, nb).view(np.float16).astype(np.float32)
+    d = (q - np.repeat(zp, 32, axis=1)).astype(np.float32) * np.repeat(s, 32, axis=1)  # exact in f32
+    return d.astype(np.float16)
+
+
+@pytest.mark.parametrize("T,N,K,zp,tile_t,wf", [(512, 640, 640, 8, 128, 4),     # BASELINE config 1
+                                                (37, 96, 640, None, 64, 5),     # ragged T and N
+                                                (1, 33, 640, None, 64, 1),      # classifier shape
+                                                (300, 640, 896, 8, 64, 5),      # O-projection K
+                                                (129, 1152, 640, None, 128, 4),  # fused QKV N
+                                                (200, 128, 640, 8, 128, 2)])    # router N
+def test_matmul_w4_vs_oracle(be, T, N, K, zp, tile_t, wf):
+    """The scale-folded GEMM of the fp16 forward path: against the oracle
+    (exact weights, per-block f32 scaling) within the fp16 bar, and against
+    the folded weights it is defined by to f32 accumulation accuracy."""
+    w = synth.qweight(300 + T, N, K, zp=zp)
+    x = synth.to_fp16_bits(synth.normal(301 + T, T * K)).reshape(T, K)
+    ref = oracle.matmul(x, w["int4"], w["scales"], w["zp"], w["bias"], N, K, x_f32=False, out_f32=True)
+    out = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 4,
+              u32s(T, N, K, 1, tile_t, wf)).view(np.float32).reshape(T, N)
+    err = rel_err_norm(out, ref)
+    print(f"w4 T={T} N={N} K={K}: rel-err vs oracle {err:.3e}")
+    assert err < 2e-3
+    xf = f16(x).astype(np.float64)
+    wf16 = folded_weights(w, N, K).astype(np.float64)
+    exact = xf @ wf16.T + f16(w["bias"]).astype(np.float64)
+    bound = K * 2.0 ** -23 * (np.abs(xf) @ np.abs(wf16).T + np.abs(f16(w["bias"])))
+    assert np.all(np.abs(out - exact) <= bound)
+
+
+def test_matmul_w4_fp16_out(be):
+    T, N, K = 70, 640, 640
+    w = synth.qweight(77, N, K, zp=8)
+    x = synth.to_fp16_bits(synth.normal(78, T * K)).reshape(T, K)
+    o32 = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 4,
+              u32s(T, N, K, 1, 64, 5)).view(np.float32)
+    o16 = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 2,
+              u32s(T, N, K, 0, 64, 5)).view(np.uint16)
+    # fp16 epilogue = the f32 result rounded as zig/math.zig:54-82 rounds
+    assert np.array_equal(o16, oracle.f32_to_fp16(o32))
+
+
 # ---------------------------------------------------------------- gather
 
 def test_embed_fixture(be, fixture):

@@ -20,21 +20,26 @@ class PfhipError(RuntimeError):
     pass
 
 
+# pfhip_model_config.precision (include/pfhip.h)
+PRECISION_FP16 = 0
+PRECISION_SPLIT = 1
+
+
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("hidden", "heads", "kv_heads", "head_dim", "window", "dff", "experts",
                                            "topk", "classes", "vocab", "layers")] + [
         ("eps", C.c_float), ("rope_theta", C.c_double), ("rope_factor", C.c_double),
         ("rope_beta_fast", C.c_double), ("rope_beta_slow", C.c_double),
-        ("rope_orig_max", C.c_uint32), ("rope_truncate", C.c_uint32)]
+        ("rope_orig_max", C.c_uint32), ("rope_truncate", C.c_uint32), ("precision", C.c_uint32)]
 
     @classmethod
-    def from_config(cls, cfg, num_layers=None, num_experts=None, vocab_size=None):
+    def from_config(cls, cfg, num_layers=None, num_experts=None, vocab_size=None, precision=PRECISION_FP16):
         r = cfg.rope
         return cls(cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.sliding_window,
                    cfg.intermediate_size, cfg.num_experts if num_experts is None else num_experts,
                    cfg.num_experts_per_tok, cfg.num_classes, cfg.vocab_size if vocab_size is None else vocab_size,
                    cfg.num_layers if num_layers is None else num_layers, cfg.rms_norm_eps, r.theta, r.factor,
-                   r.beta_fast, r.beta_slow, r.original_max_position_embeddings, int(r.truncate))
+                   r.beta_fast, r.beta_slow, r.original_max_position_embeddings, int(r.truncate), int(precision))
 
 
 # (name, restype, argtypes) of every exported entry point of include/pfhip.h
@@ -195,9 +200,11 @@ class Backend:
 class Model:
     """The whole forward (pfhip_model_*)."""
 
-    def __init__(self, backend: Backend, cfg, num_layers=None, num_experts=None, vocab_size=None):
+    def __init__(self, backend: Backend, cfg, num_layers=None, num_experts=None, vocab_size=None,
+                 precision=PRECISION_FP16):
         self.backend = backend
-        self.ccfg = ModelConfigC.from_config(cfg, num_layers, num_experts, vocab_size)
+        self.precision = int(precision)
+        self.ccfg = ModelConfigC.from_config(cfg, num_layers, num_experts, vocab_size, precision)
         self.num_classes = cfg.num_classes
         e = _err()
         h = lib().pfhip_model_create(backend.handle, C.byref(self.ccfg), e, ERR_CAP)

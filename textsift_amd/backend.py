@@ -38,12 +38,16 @@ class Logits:
 class HipBackend:
     name = "native-hip"
 
-    def __init__(self, weights: dict, config: ModelConfig = PF_CONFIG, device: int = 0):
+    def __init__(self, weights: dict, config: ModelConfig = PF_CONFIG, device: int = 0,
+                 precision: int = _native.PRECISION_FP16):
         """weights: NodeBackend-named tensors (see textsift_amd.synth) as numpy
-        arrays holding the ONNX byte layouts."""
+        arrays holding the ONNX byte layouts. precision: PRECISION_FP16 (fp16
+        GEMM inputs, the reference GPU paths' numerics) or PRECISION_SPLIT
+        (f32 GEMM inputs carried as hi/lo fp16, the WASM path's numerics)."""
         self._weights = weights
         self._cfg = config
         self._device = device
+        self._precision = int(precision)
         self._backend: _native.Backend | None = None
         self._model: _native.Model | None = None
         self.num_layers = max(int(k.split(".")[1]) for k in weights if k.startswith("layers.")) + 1
@@ -56,7 +60,7 @@ class HipBackend:
             return  # idempotent (native/backend.ts:408)
         be = _native.Backend(self._device)
         try:
-            m = _native.Model(be, self._cfg, self.num_layers, self.num_experts, self.vocab_size)
+            m = _native.Model(be, self._cfg, self.num_layers, self.num_experts, self.vocab_size, self._precision)
             try:
                 for name, arr in self._weights.items():
                     m.set_weight(name, arr)

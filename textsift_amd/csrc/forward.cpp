@@ -45,10 +45,16 @@ struct QW {  // one MatMulNBits weight on device
   const uint16_t* bias = nullptr;
 };
 
+struct W4 {  // one weight in the gemm_w4 form (w4_prepare)
+  const uint32_t* w = nullptr;
+  const uint32_t* sz = nullptr;
+};
+
 struct LayerW {
   const uint16_t* ln_in;
   const uint16_t* ln_post;
   QW qkv, o, router, gate_up, down;
+  W4 qkv4, o4, router4, gate_up4, down4;  // PFHIP_PRECISION_FP16 only
   const float* sinks;
 };
 
@@ -68,6 +74,7 @@ struct pfhip_model {
   std::map<std::string, DevT> w;            // uploaded tensors
   std::vector<DevT> owned;                  // derived tensors (fused qkv)
   std::vector<LayerW> layers;
+  W4 score4;
   bool finalized = false;
   // per-forward scratch
   void* scratch = nullptr;
@@ -107,6 +114,18 @@ const T* W(pfhip_model* m, const std::string& name) {
 QW qw(pfhip_model* m, const std::string& p) {
   return QW{W<uint8_t>(m, p + ".int4"), W<uint16_t>(m, p + ".scales"), W<uint8_t>(m, p + ".zp"),
             W<uint16_t>(m, p + ".bias")};
+}
+
+// Scale-folded copy of a MatMulNBits weight ([lead][N][K]) for gemm_w4.
+W4 prepare_w4(pfhip_model* m, const QW& q, size_t N, size_t K, size_t lead = 1) {
+  DevT tw, ts;
+  PF_HIP(hipMalloc(&tw.p, lead * N * K / 2));
+  m->owned.push_back(tw);
+  PF_HIP(hipMalloc(&ts.p, lead * N * (K / 32) * 4));
+  m->owned.push_back(ts);
+  w4_prepare(m->b, q.q, q.s, q.z, static_cast<uint32_t*>(tw.p), static_cast<uint32_t*>(ts.p), (int)(lead * N),
+             (int)K);
+  return W4{static_cast<const uint32_t*>(tw.p), static_cast<const uint32_t*>(ts.p)};
 }
 
 // YARN RoPE tables (browser/inference/rope.ts:27-144): inverse frequencies
@@ -273,9 +292,14 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     m->rope_T = T;
   }
 
+  const bool f16 = c.precision == PFHIP_PRECISION_FP16;
+  // GEMM tiles of the fp16 path: (tokens, 16-row fragments per wave)
+  const int gw_t = tt, gw_f = tt == 128 ? 4 : 5;
+
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
-  rms_norm_split(b, s.h0, m->layers[0].ln_in, s.xn_hi, s.xn_lo, M, D, c.eps);
+  if (f16) rms_norm_f16(b, s.h0, m->layers[0].ln_in, s.xn_hi, M, D, c.eps);
+  else rms_norm_split(b, s.h0, m->layers[0].ln_in, s.xn_hi, s.xn_lo, M, D, c.eps);
   uint16_t* h = s.h0;
   uint16_t* hn = s.h1;
   for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -287,7 +311,12 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.w = L.qkv.q; a.ws = L.qkv.s; a.wz = L.qkv.z; a.bias = L.qkv.bias;
       a.out = s.qkv; a.ldo = NQKV; a.M = M; a.N = NQKV; a.K = D;
       a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
-      gemm_int4(b, a, XKind::SPLIT, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
+      if (f16) {
+        a.w = reinterpret_cast<const uint8_t*>(L.qkv4.w); a.wsz = L.qkv4.sz;
+        gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, 128, 4, "gemm_qkv_rope");
+      } else {
+        gemm_int4(b, a, XKind::SPLIT, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
+      }
     }
     record_tap(m, "qkv." + tag, s.qkv, (size_t)M * NQKV * 2);
     {
@@ -306,16 +335,27 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.x = s.att; a.ldx = Hq * hd;
       a.w = L.o.q; a.ws = L.o.s; a.wz = L.o.z; a.bias = L.o.bias;
       a.out = s.o; a.ldo = D; a.M = M; a.N = D; a.K = Hq * hd;
-      gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
+      if (f16) {
+        a.w = reinterpret_cast<const uint8_t*>(L.o4.w); a.wsz = L.o4.sz;
+        gemm_w4(b, a, XKind::F16, Epi::F16, false, 64, 5, "gemm_o");
+      } else {
+        gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
+      }
     }
-    add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
+    if (f16) add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
+    else add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
     record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
     {
       GemmArgs a;
       a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
       a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
       a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
-      gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
+      if (f16) {
+        a.w = reinterpret_cast<const uint8_t*>(L.router4.w); a.wsz = L.router4.sz;
+        gemm_w4(b, a, XKind::F16, Epi::F32, false, 128, 2, "gemm_router");
+      } else {
+        gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
+      }
     }
     router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
     record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
@@ -330,7 +370,13 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       g.bias_gs = (size_t)2 * F;
       g.out = s.glu_hi; g.out_lo = s.glu_lo; g.ldo = F; g.M = M * K; g.N = 2 * F; g.K = D;
       g.tiles = plan.tiles; g.num_tiles = plan.num_tiles; g.max_tiles = plan.max_tiles;
-      gemm_int4(b, g, XKind::SPLIT, Epi::SWIGLU_SPLIT, true, tt, "gemm_moe_gate_up");
+      if (f16) {
+        g.w = reinterpret_cast<const uint8_t*>(L.gate_up4.w); g.wsz = L.gate_up4.sz;
+        g.wsz_gs = (size_t)2 * F * (D / 32);
+        gemm_w4(b, g, XKind::F16, Epi::SWIGLU_F16, true, gw_t, gw_f, "gemm_moe_gate_up");
+      } else {
+        gemm_int4(b, g, XKind::SPLIT, Epi::SWIGLU_SPLIT, true, tt, "gemm_moe_gate_up");
+      }
     }
     {
       GemmArgs d;
@@ -339,10 +385,17 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       d.w_gs = q_bytes(D, F); d.ws_gs = s_bytes(D, F) / 2; d.wz_gs = z_bytes(D, F); d.bias_gs = (size_t)D;
       d.out = s.y; d.ldo = D; d.M = M * K; d.N = D; d.K = F;
       d.tiles = plan.tiles; d.num_tiles = plan.num_tiles; d.max_tiles = plan.max_tiles;
-      gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "gemm_moe_down");
+      if (f16) {
+        d.w = reinterpret_cast<const uint8_t*>(L.down4.w); d.wsz = L.down4.sz;
+        d.wsz_gs = (size_t)D * (F / 32);
+        gemm_w4(b, d, XKind::F16, Epi::F32, true, gw_t, gw_f, "gemm_moe_down");
+      } else {
+        gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "gemm_moe_down");
+      }
     }
     const uint16_t* gamma_next = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : W<uint16_t>(m, "final_norm");
-    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn_hi, s.xn_lo, M, K, D, c.eps);
+    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn_hi, f16 ? nullptr : s.xn_lo, M,
+                     K, D, c.eps);
     record_tap(m, "h." + tag, hn, (size_t)M * D * 2);
     std::swap(h, hn);
   }
@@ -352,7 +405,12 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     QW sc = qw(m, "score");
     a.w = sc.q; a.ws = sc.s; a.wz = sc.z; a.bias = sc.bias;
     a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
-    gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
+    if (f16) {
+      a.w = reinterpret_cast<const uint8_t*>(m->score4.w); a.wsz = m->score4.sz;
+      gemm_w4(b, a, XKind::F16, Epi::F16, false, 64, 1, "gemm_classifier");
+    } else {
+      gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
+    }
   }
   record_tap(m, "logits16", s.logits16, (size_t)M * C * 2);
   // wasm.ts:776-796 widens the fp16 logits IEEE-correctly
@@ -371,6 +429,10 @@ pfhip_model* pfhip_model_create(pfhip_backend* b, const pfhip_model_config* cfg,
     PF_CHECK(c.topk >= 1 && c.topk <= 8 && c.experts >= c.topk && c.experts <= 256, "bad experts / topk");
     PF_CHECK(c.layers >= 1 && c.classes >= 1 && c.vocab >= 1, "bad layers / classes / vocab");
     PF_CHECK(c.window <= 128, "window must be <= 128");
+    PF_CHECK(c.precision == PFHIP_PRECISION_FP16 || c.precision == PFHIP_PRECISION_SPLIT, "unknown precision");
+    if (c.precision == PFHIP_PRECISION_FP16)
+      PF_CHECK(c.hidden % 128 == 0 && c.dff % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
+               "PFHIP_PRECISION_FP16 needs hidden, dff and heads*head_dim to be multiples of 128");
     pfhip_model* m = new pfhip_model();
     m->b = b;
     m->cfg = c;
@@ -485,8 +547,18 @@ int pfhip_model_finalize(pfhip_model* m, char* err, size_t cap) {
       L.gate_up = qw(m, p + "experts.gate_up");
       L.down = qw(m, p + "experts.down");
       L.sinks = W<float>(m, p + "attn.sinks");
+      if (c.precision == PFHIP_PRECISION_FP16) {
+        const size_t E = c.experts, F = c.dff;
+        L.qkv4 = prepare_w4(m, L.qkv, N, D);
+        L.o4 = prepare_w4(m, L.o, D, Nq);
+        L.router4 = prepare_w4(m, L.router, E, D);
+        L.gate_up4 = prepare_w4(m, L.gate_up, 2 * F, D, E);
+        L.down4 = prepare_w4(m, L.down, D, F, E);
+      }
       m->layers.push_back(L);
     }
+    if (c.precision == PFHIP_PRECISION_FP16) m->score4 = prepare_w4(m, qw(m, "score"), c.classes, D);
+    PF_HIP(hipStreamSynchronize(m->b->stream));
     m->finalized = true;
     return 0;
   } catch (const std::exception& ex) {

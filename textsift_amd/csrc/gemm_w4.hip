@@ -1,0 +1,405 @@
+// gemm_w4.hip — MatMulNBits int4 GEMM with the block scale folded into the
+// fp16 weights (the model forward's fast path).
+//
+// Computes out[t][n] = sum_k x[t][k] * w16[n][k] + bias[n] with
+// w16[n][k] = fp16((q[n][k] - zp[n][b]) * scale[n][b]) — MatMulNBits
+// (packages/textsift/src/zig/wasm_exports.zig:560-707) with the per-block
+// scale applied to each weight in fp16 instead of to each block's partial
+// sum in f32. The GPU paths of the reference feed these GEMMs fp16
+// activations (src/native/backend.ts:557-576); the weight rounding adds an
+// error of the same size as that activation rounding (2^-12 relative per
+// product).
+//
+// Mapping to CDNA4:
+//  * No weight staging through LDS and no per-block f32 scale update. Each
+//    wave owns WF x 16 weight rows of the tile and reads its MFMA A-operand
+//    fragments straight from HBM: lane (l16, lg) loads 16 bytes = one whole
+//    quant block (32 nibbles) of row l16 at K offset 32*lg of the current
+//    128-wide K chunk, and dequantises it in registers.
+//  * K is permuted inside each 128-wide chunk: MFMA step j (0..3) takes the
+//    8 values K = 32*lg + 8*j .. +7 from lane group lg. The activation
+//    operand uses the same permutation, so the dot product is unchanged.
+//  * Weights are repacked once (w4_repack): each dword holds k0,k2,k4,k6 in
+//    its low half's nibbles and k1,k3,k5,k7 in its high half's, so one
+//    shift + and_or per pair produces (1024 + q) as packed fp16 in natural
+//    k order; one packed add subtracts (1024 + zp) exactly and one packed
+//    multiply applies the scale (the only rounding).
+//  * Activations are the shared operand: the workgroup's BT x 128 chunk is
+//    copied HBM -> LDS with global_load_lds_dwordx4 (no register staging),
+//    double buffered, in 256-byte rows whose 16-byte units are XOR-swizzled
+//    by (row & 15) so the MFMA B-fragment reads (ds_read_b128) are
+//    conflict-free.
+//  * The GEMM is computed transposed (D = W . X^T) as in gemm_int4.hip, so
+//    each lane ends with 4 consecutive output columns of one token and the
+//    RoPE / SwiGLU epilogues are lane-local.
+#include "common.cuh"
+#include "pfhip_internal.h"
+
+namespace pf {
+
+namespace {
+
+constexpr int KC = 128;  // K per chunk (4 quant blocks, 256 bytes of fp16 activations per row)
+constexpr int NW = 4;    // waves per workgroup, stacked along N
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i's bytes
+// land at dst + 16 i; dst must be wave-uniform. The builtin exists only for
+// the device pass (clang drops the kernel's host stub if the host pass sees it).
+__device__ __forceinline__ void copy16_to_lds(const void* src, lds_ptr_t dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+#endif
+}
+
+__device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// One repacked dword (8 nibbles) -> fp16 (q - zp) * scale for k = 0..7.
+// off = (-(1024 + zp), -(1024 + zp)), sc = (scale, scale).
+__device__ __forceinline__ h8_t dequant_fold(uint32_t w, h2_t off, h2_t sc) {
+  const uint32_t p0 = (w & 0x000F000Fu) | 0x64006400u;
+  const uint32_t p1 = ((w >> 4) & 0x000F000Fu) | 0x64006400u;
+  const uint32_t p2 = ((w >> 8) & 0x000F000Fu) | 0x64006400u;
+  const uint32_t p3 = ((w >> 12) & 0x000F000Fu) | 0x64006400u;
+  const h2_t d0 = (__builtin_bit_cast(h2_t, p0) + off) * sc;
+  const h2_t d1 = (__builtin_bit_cast(h2_t, p1) + off) * sc;
+  const h2_t d2 = (__builtin_bit_cast(h2_t, p2) + off) * sc;
+  const h2_t d3 = (__builtin_bit_cast(h2_t, p3) + off) * sc;
+  return __builtin_bit_cast(h8_t, u4_t{h2_bits(d0), h2_bits(d1), h2_bits(d2), h2_bits(d3)});
+}
+
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int per = total >> 3, rem = total & 7;
+  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED>
+__global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
+  constexpr int BN = NW * WF * 16;  // weight rows per workgroup
+  constexpr int TJ = BT / 16;       // token fragments per wave
+  constexpr int XI = BT / 16;       // 1 KB direct loads per wave per plane per chunk
+  constexpr int PLANE = BT * KC;    // halves per plane per buffer
+
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [2][XS][BT][KC] swizzled
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+
+  const int n_tiles = (p.N + BN - 1) / BN;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int nt = bid % n_tiles;
+  const int tt = bid / n_tiles;
+  int expert = 0, row0, rows;
+  if constexpr (GROUPED) {
+    if (tt >= *p.num_tiles) return;
+    const int4 ti = reinterpret_cast<const int4*>(p.tiles)[tt];
+    expert = ti.x;
+    row0 = ti.y;
+    rows = ti.z;
+  } else {
+    row0 = tt * BT;
+    rows = min(BT, p.M - row0);
+    if (rows <= 0) return;
+  }
+  const int n0 = nt * BN;
+  const int K = p.K;
+  const int C = K / KC;
+  const int kd = K >> 3;   // dwords per packed weight row
+  const int nb = K >> 5;   // quant blocks per row
+
+  // ---- weight fragment pointers (rows past N read row N-1; never stored)
+  const uint32_t* __restrict__ W = reinterpret_cast<const uint32_t*>(p.w + (size_t)expert * p.w_gs);
+  const uint32_t* __restrict__ SZ = p.wsz + (size_t)expert * p.wsz_gs;
+  const uint32_t* wptr[WF];
+  const uint32_t* sptr[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) {
+    const int n = min(n0 + (wave * WF + f) * 16 + l16, p.N - 1);
+    wptr[f] = W + (size_t)n * kd + lg * 4;
+    sptr[f] = SZ + (size_t)n * nb + lg;
+  }
+
+  // ---- activation rows this lane copies (rows past the tile read the
+  // tile's last row; their outputs are never stored)
+  const uint16_t* __restrict__ xsrc[XS];
+  xsrc[0] = static_cast<const uint16_t*>(p.x);
+  if constexpr (XS == 2) xsrc[1] = p.x_lo;
+  int xoff[XI];
+#pragma unroll
+  for (int m = 0; m < XI; ++m) {
+    const int r = (m * NW + wave) * 4 + lg;
+    const int lr = row0 + min(r, rows - 1);
+    const int g = p.row_map ? p.row_map[lr] : lr;
+    xoff[m] = g * p.ldx + ((l16 ^ (r & 15)) << 3);
+  }
+
+  auto load_x = [&](int c, int buf) {
+#pragma unroll
+    for (int pl = 0; pl < XS; ++pl)
+#pragma unroll
+      for (int m = 0; m < XI; ++m) {
+        _Float16* dst = xs_lds + (buf * XS + pl) * PLANE + (m * NW + wave) * 512;
+        copy16_to_lds(xsrc[pl] + xoff[m] + c * KC, (lds_ptr_t)dst);
+      }
+  };
+
+  u4_t wraw[WF], wnext[WF];
+  uint32_t sz[WF], sznext[WF];
+  auto load_w = [&](int c, u4_t* wr, uint32_t* s) {
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      wr[f] = *reinterpret_cast<const u4_t*>(wptr[f] + c * 16);
+      s[f] = sptr[f][c * 4];
+    }
+  };
+
+  f4_t acc[WF][TJ];
+#pragma unroll
+  for (int f = 0; f < WF; ++f)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  load_x(0, 0);
+  load_w(0, wraw, sz);
+  for (int c = 0; c < C; ++c) {
+    const int buf = c & 1;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (c + 1 < C) {
+      load_x(c + 1, buf ^ 1);
+      load_w(c + 1, wnext, sznext);
+    }
+    h2_t off[WF], sc[WF];
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      const h2_t pr = __builtin_bit_cast(h2_t, sz[f]);
+      off[f] = h2_t{pr.x, pr.x};
+      sc[f] = h2_t{pr.y, pr.y};
+    }
+    const _Float16* xb = xs_lds + buf * XS * PLANE;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h8_t wd[WF];
+#pragma unroll
+      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wraw[f][j], off[f], sc[f]);
+      const int unit = ((4 * lg + j) ^ l16) << 3;
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) {
+        const int o = (16 * tj + l16) * KC + unit;
+        const h8_t xh = *reinterpret_cast<const h8_t*>(xb + o);
+#pragma unroll
+        for (int f = 0; f < WF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xh, acc[f][tj]);
+        if constexpr (XS == 2) {
+          const h8_t xl = *reinterpret_cast<const h8_t*>(xb + PLANE + o);
+#pragma unroll
+          for (int f = 0; f < WF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xl, acc[f][tj]);
+        }
+      }
+    }
+    if (c + 1 < C) {
+#pragma unroll
+      for (int f = 0; f < WF; ++f) {
+        wraw[f] = wnext[f];
+        sz[f] = sznext[f];
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds out[token = 16 tj + l16][n = n0 + (wave WF + f) 16 + 4 lg + r]
+  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
+#pragma unroll
+  for (int f = 0; f < WF; ++f) {
+    const int n = n0 + (wave * WF + f) * 16 + 4 * lg;
+    if (n >= p.N) continue;
+    float bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[r] = (BIAS && n + r < p.N) ? wasm_h2f(BIAS[n + r]) : 0.0f;
+#pragma unroll
+    for (int tj = 0; tj < TJ; ++tj) {
+      const int lt = 16 * tj + l16;
+      if (lt >= rows) continue;
+      const size_t orow = (size_t)(row0 + lt);
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[f][tj][r] + bv[r];
+      if constexpr (EPI == Epi::F32) {
+        float* o = static_cast<float*>(p.out) + orow * p.ldo + n;
+        if (n + 3 < p.N) {
+          *reinterpret_cast<f4_t*>(o) = f4_t{v[0], v[1], v[2], v[3]};
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) o[r] = v[r];
+        }
+      } else if constexpr (EPI == Epi::F16 || EPI == Epi::ROPE_F16) {
+        uint16_t hb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hb[r] = wasm_f2h(v[r]);
+        if constexpr (EPI == Epi::ROPE_F16) {
+          if (n < p.rope_cols) {
+            // rope_apply (zig/wasm_exports.zig:1460-1502) on the fp16 values:
+            // each product rounded to fp16, combined in f32, rounded again.
+            const int pos = (int)(orow % (size_t)p.seq_len);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int pidx = ((n & 63) >> 1) + h;
+              const float cs = wasm_h2f(p.rope_cos[pos * 32 + pidx]);
+              const float sn = wasm_h2f(p.rope_sin[pos * 32 + pidx]);
+              const float a = wasm_h2f(hb[2 * h]), bb = wasm_h2f(hb[2 * h + 1]);
+              const float ac = wasm_h2f(wasm_f2h(a * cs)), bs = wasm_h2f(wasm_f2h(bb * sn));
+              const float bc = wasm_h2f(wasm_f2h(bb * cs)), as_ = wasm_h2f(wasm_f2h(a * sn));
+              hb[2 * h] = wasm_f2h(ac - bs);
+              hb[2 * h + 1] = wasm_f2h(bc + as_);
+            }
+          }
+        }
+        uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
+        if (n + 3 < p.N) {
+          *reinterpret_cast<u2_t*>(o) = u2_t{(uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
+                                             (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) o[r] = hb[r];
+        }
+      } else {  // SwiGLU: (gate, up) interleaved columns -> glu column n/2
+        const float g0 = swiglu_clamp(v[0], v[1]);
+        const float g1 = swiglu_clamp(v[2], v[3]);
+        const size_t oc = (size_t)(n >> 1);
+        if constexpr (EPI == Epi::SWIGLU_SPLIT) {
+          uint16_t a0, a1, e0, e1;
+          split_hilo(g0, a0, e0);
+          split_hilo(g1, a1, e1);
+          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) =
+              (uint32_t)a0 | ((uint32_t)a1 << 16);
+          *reinterpret_cast<uint32_t*>(p.out_lo + orow * p.ldo + oc) = (uint32_t)e0 | ((uint32_t)e1 << 16);
+        } else {
+          uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
+          *reinterpret_cast<uint32_t*>(o) = (uint32_t)wasm_f2h(g0) | ((uint32_t)wasm_f2h(g1) << 16);
+        }
+      }
+    }
+  }
+}
+
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED>
+void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
+  constexpr int BN = NW * WF * 16;
+  const int n_tiles = (a.N + BN - 1) / BN;
+  const int t_tiles = GROUPED ? a.max_tiles : (a.M + BT - 1) / BT;
+  const long grid = (long)n_tiles * t_tiles;
+  if (grid == 0) return;
+  PF_CHECK(grid < (1L << 31), "gemm_w4: grid too large");
+  const size_t lds = (size_t)2 * XS * BT * KC * sizeof(uint16_t);
+  static bool attr_set = false;  // per template instance
+  if (!attr_set) {
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr_set = true;
+  }
+  ProfScope ps(b, name);
+  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED>), dim3((unsigned)grid), dim3(256), lds, b->stream, a);
+  PF_HIP(hipGetLastError());
+}
+
+template <int WF, int BT, int XS, bool GROUPED>
+void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name) {
+  switch (epi) {
+    case Epi::F16: return launch<WF, BT, XS, Epi::F16, GROUPED>(b, a, name);
+    case Epi::F32: return launch<WF, BT, XS, Epi::F32, GROUPED>(b, a, name);
+    case Epi::ROPE_F16: return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED>(b, a, name);
+    case Epi::SWIGLU_SPLIT: break;
+    case Epi::SWIGLU_F16: return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED>(b, a, name);
+  }
+  throw Error("gemm_w4: unsupported epilogue");
+}
+
+template <int WF, int BT>
+void dispatch_grouped(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped, const char* name) {
+  if (grouped) dispatch_epi<WF, BT, 1, true>(b, a, epi, name);
+  else dispatch_epi<WF, BT, 1, false>(b, a, epi, name);
+}
+
+// ---------------------------------------------------------------- weight prep
+
+// MatMulNBits bytes [G][N][K/2] (low nibble = even k) -> repacked dwords:
+// per 8 values, k0,k2,k4,k6 in nibbles 0-3 and k1,k3,k5,k7 in nibbles 4-7.
+__global__ void k_w4_repack(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t w = src[i];
+  uint32_t r = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (w >> (8 * b)) & 0xFFu;
+    r |= (byte & 0xFu) << (4 * b);          // k = 2b   -> low half
+    r |= (byte >> 4) << (16 + 4 * b);       // k = 2b+1 -> high half
+  }
+  dst[i] = r;
+}
+
+// fp16 scales [G][N][nb] + packed zero-points [G][N][ceil(nb/2)] (NULL = 0)
+// -> per block: low half fp16 -(1024 + zp), high half the fp16 scale.
+__global__ void k_w4_scale_pairs(const uint16_t* __restrict__ ws, const uint8_t* __restrict__ wz,
+                                 uint32_t* __restrict__ out, int rows, int nb) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)rows * nb) return;
+  const size_t row = i / nb;
+  const int blk = (int)(i % nb);
+  uint32_t zp = 0;
+  if (wz) {
+    const uint8_t zb = wz[row * ((nb + 1) >> 1) + (blk >> 1)];
+    zp = (blk & 1) ? (zb >> 4) : (zb & 0xFu);
+  }
+  const _Float16 off = (_Float16)(-(1024.0f + (float)zp));
+  out[i] = (uint32_t)__builtin_bit_cast(uint16_t, off) | ((uint32_t)ws[i] << 16);
+}
+
+}  // namespace
+
+void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t, int wf,
+             const char* prof_name) {
+  PF_CHECK(a.K > 0 && a.K % KC == 0, "gemm_w4: K must be a positive multiple of 128");
+  PF_CHECK(a.N > 0, "gemm_w4: N must be positive");
+  PF_CHECK(a.x && a.w && a.wsz && a.out, "gemm_w4: null operand");
+  PF_CHECK(a.ldx % 8 == 0, "gemm_w4: activation row stride must allow 16-byte loads");
+  PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
+           "gemm_w4: activations and weights must be 16-byte aligned");
+  PF_CHECK((long)a.M * a.ldx < (1L << 31) || grouped, "gemm_w4: activation offsets exceed 32 bits");
+  if (xk == XKind::SPLIT)
+    PF_CHECK(a.x_lo && (reinterpret_cast<uintptr_t>(a.x_lo) & 15) == 0, "gemm_w4: SPLIT needs an aligned lo plane");
+  if (epi == Epi::SWIGLU_SPLIT || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_w4: SwiGLU needs N % 4 == 0");
+  if (epi == Epi::SWIGLU_SPLIT) PF_CHECK(a.out_lo, "gemm_w4: SWIGLU_SPLIT needs an output lo plane");
+  if (epi == Epi::ROPE_F16)
+    PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
+             "gemm_w4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
+  if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_w4: grouped mode needs a tile list");
+  else PF_CHECK(a.M >= 0, "gemm_w4: M must be non-negative");
+  PF_CHECK(xk == XKind::F16, "gemm_w4: activations must be one fp16 plane");
+  PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
+  if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, a, epi, grouped, prof_name);
+  if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, a, epi, grouped, prof_name);
+  if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, a, epi, grouped, prof_name);
+  if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, a, epi, grouped, prof_name);
+  throw Error("gemm_w4: unsupported (tile_t, wf) = (" + std::to_string(tile_t) + ", " + std::to_string(wf) + ")");
+}
+
+void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const uint8_t* wz, uint32_t* w_out,
+                uint32_t* sz_out, int rows, int K) {
+  PF_CHECK(rows > 0 && K > 0 && K % 32 == 0, "w4_prepare: bad shape");
+  PF_CHECK((reinterpret_cast<uintptr_t>(w) & 3) == 0, "w4_prepare: weights must be 4-byte aligned");
+  const size_t nd = (size_t)rows * (K / 8);
+  const int nb = K / 32;
+  ProfScope ps(b, "w4_prepare");
+  hipLaunchKernelGGL(k_w4_repack, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, b->stream,
+                     reinterpret_cast<const uint32_t*>(w), w_out, nd);
+  PF_HIP(hipGetLastError());
+  const size_t ns = (size_t)rows * nb;
+  hipLaunchKernelGGL(k_w4_scale_pairs, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, b->stream, ws, wz, sz_out,
+                     rows, nb);
+  PF_HIP(hipGetLastError());
+}
+
+}  // namespace pf

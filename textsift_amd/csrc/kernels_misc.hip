@@ -341,7 +341,8 @@ __global__ __launch_bounds__(256) void k_moe_scatter(const int32_t* __restrict__
 // fused multiply-adds, then rounds to fp16 and adds the residual.
 // The reference weights by softmax/K and rescales by K at the end; both are
 // exact powers of two, so weighting by the softmax directly is bit-identical.
-template <bool NORM>
+// NMODE: -1 = no norm; OUT_F16 / OUT_SPLIT = form of the next block's norm output.
+template <int NMODE>
 __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                      const int32_t* __restrict__ slot_of, const float* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
@@ -383,14 +384,14 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     }
     ss += hv * hv;
   }
-  if constexpr (NORM) {
+  if constexpr (NMODE >= 0) {
     // the next block's rms_norm_fp16_to_f32 on the new residual row (:220-270)
     ss = wave_sum(ss);
     const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
 #pragma unroll
     for (int i = 0; i < MAXPL; ++i) {
       const int d = i * 64 + lane;
-      if (d < D) put<OUT_SPLIT>(norm_hi, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(gamma[d]));
+      if (d < D) put<NMODE>(norm_hi, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(gamma[d]));
     }
   }
 }
@@ -526,6 +527,16 @@ void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, c
   PF_HIP(hipGetLastError());
 }
 
+void add_rms_norm_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
+                      uint16_t* norm_out, int T, int D, float eps) {
+  PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
+  if (T <= 0) return;
+  ProfScope ps(b, "add_rmsnorm_f16");
+  hipLaunchKernelGGL(k_add_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out,
+                     norm_out, nullptr, T, D, eps);
+  PF_HIP(hipGetLastError());
+}
+
 void add_rms_norm_split(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g,
                         uint16_t* sum_out, uint16_t* hi, uint16_t* lo, int T, int D, float eps) {
   PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
@@ -651,7 +662,7 @@ void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int
   PF_CHECK(D <= 64 * MAXPL && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine");
-  hipLaunchKernelGGL(k_moe_combine<false>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
+  hipLaunchKernelGGL(k_moe_combine<-1>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
                      moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
   PF_HIP(hipGetLastError());
 }
@@ -662,8 +673,12 @@ void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, cons
   PF_CHECK(D <= 64 * MAXPL && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine_norm");
-  hipLaunchKernelGGL(k_moe_combine<true>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
-                     nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
+  if (norm_lo)
+    hipLaunchKernelGGL(k_moe_combine<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y,
+                       residual, nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
+  else
+    hipLaunchKernelGGL(k_moe_combine<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y,
+                       residual, nullptr, h_out, gamma, norm_hi, nullptr, T, K, D, eps);
   PF_HIP(hipGetLastError());
 }
 

@@ -97,6 +97,9 @@ struct GemmArgs {
   const uint8_t* wz = nullptr;   // [N][ceil(K/64)] packed uint4 zero-points, NULL = 0
   const uint16_t* bias = nullptr;  // [N] fp16, NULL = 0
   size_t w_gs = 0, ws_gs = 0, wz_gs = 0, bias_gs = 0;  // per-expert strides (elements)
+  // gemm_w4 only: repacked weights in w, and per block (fp16 -(1024+zp), fp16 scale)
+  const uint32_t* wsz = nullptr;  // [N][K/32]
+  size_t wsz_gs = 0;
   void* out = nullptr;
   uint16_t* out_lo = nullptr;    // SWIGLU_SPLIT: lo plane of the output
   int ldo = 0;
@@ -115,6 +118,15 @@ struct GemmArgs {
 void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
                const char* prof_name);
 
+// Scale-folded int4 GEMM (gemm_w4.hip): weights prepared by w4_prepare;
+// K % 128 == 0. tile_t x wf selects the tile (BT tokens x 64*wf rows).
+void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t, int wf,
+             const char* prof_name);
+// MatMulNBits weight [rows][K/2] + scales + zero-points -> the gemm_w4 form:
+// w_out [rows][K/8] repacked dwords, sz_out [rows][K/32] (offset, scale) pairs.
+void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const uint8_t* wz, uint32_t* w_out,
+                uint32_t* sz_out, int rows, int K);
+
 // GatherBlockQuantized embedding: out fp16 [T][D].
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D);
@@ -127,6 +139,8 @@ void rms_norm_split(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint
                     float eps);
 void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
                       float* norm_out, int T, int D, float eps);
+void add_rms_norm_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
+                      uint16_t* norm_out, int T, int D, float eps);
 void add_rms_norm_split(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g,
                         uint16_t* sum_out, uint16_t* hi, uint16_t* lo, int T, int D, float eps);
 // f32 -> (hi, lo) fp16 planes.
@@ -161,6 +175,7 @@ MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t);
 void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const MoePlan& plan);
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                  const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D);
+// norm_lo == NULL: the norm output is one fp16 plane in norm_hi.
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                       const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps);

@@ -291,6 +291,38 @@ static std::vector<KernelEntry>& registry() {
   r.push_back({"matmul_int4_fp16_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  run_matmul(b, bs, p, false, true, "matmul_int4_fp16_f32");
                }});
+  // matmul_int4_w4: the scale-folded GEMM of the fp16 forward path (gemm_w4).
+  // push {T, N, K, out_f32, tile_t, wf}; bindings [x fp16, w, scales, zp, bias, out]
+  r.push_back({"matmul_int4_w4", 6, 24, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), N = (int)pu(p, 1), K = (int)pu(p, 2);
+                 const bool out_f32 = pu(p, 3) != 0;
+                 const int tile_t = (int)pu(p, 4), wf = (int)pu(p, 5);
+                 PF_CHECK(K % 128 == 0, "matmul_int4_w4: K must be a multiple of 128");
+                 const int nb = K / 32;
+                 need(bs, 0, (size_t)T * K * 2, "matmul_int4_w4");
+                 need(bs, 1, (size_t)N * K / 2, "matmul_int4_w4");
+                 need(bs, 2, (size_t)N * nb * 2, "matmul_int4_w4");
+                 need(bs, 3, (size_t)N * ((nb + 1) / 2), "matmul_int4_w4");
+                 need(bs, 4, (size_t)N * 2, "matmul_int4_w4");
+                 need(bs, 5, (size_t)T * N * (out_f32 ? 4 : 2), "matmul_int4_w4");
+                 const size_t wbytes = ((size_t)N * K / 2 + 255) & ~(size_t)255;
+                 char* prep = static_cast<char*>(backend_scratch(b, wbytes + (size_t)N * nb * 4));
+                 uint32_t* w4 = reinterpret_cast<uint32_t*>(prep);
+                 uint32_t* sz = reinterpret_cast<uint32_t*>(prep + wbytes);
+                 w4_prepare(b, bp<uint8_t>(bs, 1), bp<uint16_t>(bs, 2), bp<uint8_t>(bs, 3), w4, sz, N, K);
+                 GemmArgs a;
+                 a.x = bs[0]->ptr;
+                 a.ldx = K;
+                 a.w = reinterpret_cast<const uint8_t*>(w4);
+                 a.wsz = sz;
+                 a.bias = bp<uint16_t>(bs, 4);
+                 a.out = bs[5]->ptr;
+                 a.ldo = N;
+                 a.M = T;
+                 a.N = N;
+                 a.K = K;
+                 gemm_w4(b, a, XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, tile_t, wf, "matmul_int4_w4");
+               }});
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), K = (int)pu(p, 1), E = (int)pu(p, 2), tt = (int)pu(p, 3);
