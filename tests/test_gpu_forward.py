@@ -90,9 +90,24 @@ def test_per_layer_taps_vs_oracle_block(small):
                                             sn.ctypes.data_as(C.c_void_p), None, T, 1)
         assert rc == 0
         gpu_h = m.tap(f"h.{l}", np.uint16, T * D).reshape(T, D)
-        err = rel_err_norm(f16(gpu_h), f16(out))
-        print(f"layer {l}: rel-err {err:.3e}")
-        assert err < 2e-3, f"layer {l}: {err}"
+        g, o = f16(gpu_h), f16(out)
+        err = rel_err_norm(g, o)
+        # Tokens whose 4th and 5th router logits (GPU) nearly tie may pick a
+        # different 4th expert than the oracle; the perturbation of fp16 GEMM
+        # inputs moves router logits by 1e-4 .. 1e-3. Every large per-token error
+        # must be such a near tie, near ties must be rare, and the remaining
+        # tokens must meet the bar.
+        rl = m.tap(f"router.{l}", np.float32, T * E).reshape(T, E)
+        srt = -np.sort(-rl, axis=1)
+        near_tie = (srt[:, 3] - srt[:, 4]) < 3e-3
+        tok_err = np.linalg.norm(g - o, axis=1) / np.linalg.norm(o, axis=1)
+        rest = rel_err_norm(g[~near_tie], o[~near_tie])
+        print(f"layer {l}: rel-err {err:.3e}; near-tie tokens {int(near_tie.sum())}, rel-err of the rest {rest:.3e}")
+        assert np.all(near_tie[tok_err > 5e-3]), f"layer {l}: large error on a token without a routing near-tie"
+        assert near_tie.mean() <= 0.03
+        assert rest < 2e-3, f"layer {l}: {rest}"
+        if be.precision == _native.PRECISION_SPLIT:
+            assert err < 2e-3, f"layer {l}: {err}"
         h_in = gpu_h  # next block starts from the GPU's residual
     m.enable_taps(False)
 

@@ -99,6 +99,10 @@ class HipBackend:
         return data.reshape(B, T, self._cfg.num_classes)
 
     @property
+    def precision(self) -> int:
+        return self._precision
+
+    @property
     def model(self) -> _native.Model:
         return self._model
 

@@ -24,62 +24,115 @@
 //  * p is normalised before P.V (as the reference does) and enters the
 //    MFMA as an fp16 hi + lo pair, so P.V carries ~22 significant bits.
 #include "common.cuh"
+#include "epilogue.cuh"
 #include "pfhip_internal.h"
 
 namespace pf {
 
 namespace {
 
-constexpr int QB = 64;  // query tokens per workgroup (4 waves x 16)
+// exp_approx with the final scaling done by ldexp. The two differ only when
+// floor(x log2 e) = -127 (x < -87.3): exp_approx returns 0 there, this a
+// value below 2^-126. Such a term is below 2^-126 of the row maximum's (which
+// is 1), so it leaves the f32 row sum unchanged and its probability rounds
+// to fp16 zero in both hi and lo: the attention output is identical.
+__device__ __forceinline__ float exp_softmax(float x) {
+  const float LOG2_E = 1.44269504088896340736f;
+  const float y = fmaxf(x, -88.0f) * LOG2_E;
+  const float fl = floorf(y);
+  const float frac = y - fl;
+  float poly = fmaf(0.001333355f, frac, 0.009679494f);
+  poly = fmaf(poly, frac, 0.055053319f);
+  poly = fmaf(poly, frac, 0.240226522f);
+  poly = fmaf(poly, frac, 0.693154774f);
+  poly = fmaf(poly, frac, 1.000000012f);
+  return __builtin_amdgcn_ldexpf(poly, (int)fl);
+}
 
-template <int HD, int NCH>
-__global__ __launch_bounds__(256) void k_banded_attention(AttnArgs a) {
-  constexpr int ROWS = 48 + 32 * NCH;   // staged key rows (covers every wave's chunks)
-  constexpr int LDK = HD + 8;           // K row stride (halves)
-  constexpr int LDV = ROWS + 8;         // V^T row stride (halves)
-  constexpr int NDH = HD / 32;          // MFMA K-steps over head_dim for Q.K
-  constexpr int NDT = HD / 16;          // 16-row dim tiles of O^T
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// NW waves x 16 queries per workgroup; NCH 32-key chunks per 16-query tile.
+template <int HD, int NCH, int NW>
+__global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
+  constexpr int QB = 16 * NW;                // query tokens per workgroup
+  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
+  constexpr int LDK = HD + 8;                // K row stride (halves)
+  constexpr int LDV = ROWS + 8;              // V^T row stride (halves)
+  constexpr int NDH = HD / 32;               // MFMA K-steps over head_dim for Q.K
+  constexpr int NDT = HD / 16;               // 16-row dim tiles of O^T
+  static_assert(ROWS % 4 == 0, "V^T staging writes 4 keys at a time");
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
-  _Float16* Ks = smem;                  // [ROWS][LDK]
-  _Float16* Vt = smem + ROWS * LDK;     // [HD][LDV]
+  _Float16* Ks = smem;                       // [ROWS][LDK]
+  _Float16* Vt = smem + ROWS * LDK;          // [HD][LDV]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int t0 = blockIdx.x * QB;
-  const int g = blockIdx.y;             // kv head
+  const int g = blockIdx.y;                  // kv head
   const int bseq = blockIdx.z;
   const int T = a.T, W = a.window;
   const size_t seq0 = (size_t)bseq * T;
-  const int kbase = t0 - W;             // key index of staged row 0
+  const int kbase = t0 - W;                  // key index of staged row 0
 
-  // ---- stage K and V^T (rows outside [0, T) are zero and masked later)
-  for (int i = tid; i < ROWS * (HD / 8); i += 256) {
+  // ---- stage K (row-major) and V^T; rows outside [0, T) are zero (masked later)
+  for (int i = tid; i < ROWS * (HD / 8); i += 64 * NW) {
     const int r = i / (HD / 8), c = i % (HD / 8);
     const int key = kbase + r;
-    u4_t kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-    if (key >= 0 && key < T) {
-      kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
-      vv = *reinterpret_cast<const u4_t*>(a.v + (seq0 + key) * a.v_stride + g * HD + c * 8);
-    }
+    u4_t kv = {0u, 0u, 0u, 0u};
+    if (key >= 0 && key < T) kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
     *reinterpret_cast<u4_t*>(&Ks[r * LDK + c * 8]) = kv;
-    const h8_t vh = __builtin_bit_cast(h8_t, vv);
+  }
+  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += 64 * NW) {  // 4 keys x 8 dims per thread
+    const int r4 = (i / (HD / 8)) * 4, c = i % (HD / 8);
+    h8_t vh[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) Vt[(c * 8 + j) * LDV + r] = vh[j];
+    for (int u = 0; u < 4; ++u) {
+      const int key = kbase + r4 + u;
+      u4_t vv = {0u, 0u, 0u, 0u};
+      if (key >= 0 && key < T) vv = *reinterpret_cast<const u4_t*>(a.v + (seq0 + key) * a.v_stride + g * HD + c * 8);
+      vh[u] = __builtin_bit_cast(h8_t, vv);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<h4_t*>(&Vt[(c * 8 + j) * LDV + r4]) = h4_t{vh[0][j], vh[1][j], vh[2][j], vh[3][j]};
   }
   __syncthreads();
 
-  const int tq0 = t0 + 16 * wave;       // this wave's first query
-  const int tq = tq0 + l16;             // this lane's query
-  const int rb = 16 * wave;             // staged row of key tq0 - W
+  const int tq0 = t0 + 16 * wave;            // this wave's first query
+  const int tq = tq0 + l16;                  // this lane's query
+  const int rb = 16 * wave;                  // staged row of key tq0 - W
+  const int kw = tq0 - W;                    // key at chunk offset 0 of this wave
+  const bool q_ok = tq < T;
   const int ws = max(0, tq - W), we = min(T, tq + W + 1);
   const int n_keys = we - ws;
   const int total = n_keys + 1;
-  const int vec_end = total - (total & 3);  // reference's 4-lane part vs scalar tail
+  const int vec_end = total - (total & 3);   // reference's 4-lane part vs scalar tail
+  // window [lo, hi) and scalar tail [tail, hi) as chunk offsets
+  const int lo0 = ws - kw, hi0 = we - kw, tail0 = ws + vec_end - kw;
+  // wave-uniform chunk classes (lanes past T do not constrain them)
+  const int full_lo = wave_max_i(q_ok ? lo0 : 0);
+  const int full_hi = wave_min_i(q_ok ? hi0 : 1 << 20);
+  const int tail_lo = wave_min_i(q_ok ? tail0 : 1 << 20);
+  const int any_hi = wave_max_i(q_ok ? hi0 : 0);
+  const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
-  const bool q_ok = tq < T;
 
   for (int hh = 0; hh < G; ++hh) {
     const int hq = g * G + hh;
+    // Opaque per-head copies of the window bounds: comparisons against them
+    // are then recomputed per head instead of being hoisted out of the loop
+    // as dozens of live lane masks (which spill).
+    int lo = lo0, hi = hi0, tail = tail0;
+    asm volatile("" : "+v"(lo), "+v"(hi), "+v"(tail));
     // Q fragment (B operand): Q[tq][32 dh + 8 lg .. +8]
     h8_t qf[NDH];
 #pragma unroll
@@ -90,29 +143,45 @@ __global__ __launch_bounds__(256) void k_banded_attention(AttnArgs a) {
     }
     const float sink = a.sinks ? a.sinks[hq] : -INFINITY;
 
-    // ---- pass 1: scores for the whole band, kept in registers
+    // ---- pass 1: scores for the whole band, kept in registers. Slots
+    // outside the query's window hold NaN; masked keys hold -inf.
     float s[NCH][2][4];
     float m = sink;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
+      f4_t acc[2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        f4_t acc = {0.f, 0.f, 0.f, 0.f};
+        acc[kt] = f4_t{0.f, 0.f, 0.f, 0.f};
         const int row = rb + 32 * c + 16 * kt + l16;
 #pragma unroll
         for (int dh = 0; dh < NDH; ++dh) {
           const h8_t kf = *reinterpret_cast<const h8_t*>(&Ks[row * LDK + 32 * dh + 8 * lg]);
-          acc = mfma16x16x32(kf, qf[dh], acc);
+          acc[kt] = mfma16x16x32(kf, qf[dh], acc[kt]);
         }
+      }
+      if (!masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi) {  // every slot in every window
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = tq0 - W + 32 * c + 16 * kt + 4 * lg + r;
-          bool valid = key >= ws && key < we;
-          if (valid && a.mask) valid = a.mask[seq0 + key] != 0;
-          const float sv = valid ? acc[r] * a.scale : -INFINITY;
-          s[c][kt][r] = (key >= ws && key < we) ? sv : NAN;  // NAN marks "not in this query's window"
-          if (valid) m = fmaxf(m, sv);
-        }
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sv = acc[kt][r] * a.scale;
+            s[c][kt][r] = sv;
+            m = fmaxf(m, sv);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = 32 * c + 16 * kt + 4 * lg + r;
+            const bool inwin = (off >= lo) & (off < hi);
+            bool valid = inwin;
+            if (masked) valid = valid && a.mask[seq0 + kw + off] != 0;
+            const float sv = valid ? acc[kt][r] * a.scale : -INFINITY;
+            s[c][kt][r] = inwin ? sv : NAN;
+            m = valid ? fmaxf(m, sv) : m;
+          }
       }
       // keep the scheduler from hoisting every chunk's LDS loads (spills)
       __builtin_amdgcn_sched_barrier(0);
@@ -121,26 +190,41 @@ __global__ __launch_bounds__(256) void k_banded_attention(AttnArgs a) {
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
 
-    // ---- pass 2: exp (polynomial in the reference's vector part, libm in its tail) and sum
+    // ---- pass 2: exp (polynomial in the reference's vector part, libm in
+    // its scalar tail) and the row sum
     float l = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCH; ++c) {
+      const bool plain = !masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi &&
+                         !(32 * c + 32 > tail_lo && 32 * c < any_hi);
+      if (plain) {  // wave-uniform: every slot in every window, no tail key
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float sv = s[c][kt][r];
-          float e = 0.0f;
-          if (!(sv != sv)) {
-            const int i = tq0 - W + 32 * c + 16 * kt + 4 * lg + r - ws;
-            e = i < vec_end ? exp_approx(sv - m) : expf(sv - m);
+          for (int r = 0; r < 4; ++r) {
+            const float e = exp_softmax(s[c][kt][r] - m);
+            s[c][kt][r] = e;
+            l += e;
           }
-          s[c][kt][r] = e;
-          l += e;
-        }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sv = s[c][kt][r];
+            const float x = sv - m;
+            const int off = 32 * c + 16 * kt + 4 * lg + r;
+            float e = off >= tail ? expf(x) : exp_softmax(x);
+            e = (sv != sv) ? 0.0f : e;
+            s[c][kt][r] = e;
+            l += e;
+          }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    l += n_keys < vec_end ? exp_approx(sink - m) : expf(sink - m);
+    l += n_keys < vec_end ? exp_softmax(sink - m) : expf(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 
     // ---- pass 3: O^T = V^T . P^T with P normalised, as fp16 hi + lo
@@ -155,9 +239,9 @@ __global__ __launch_bounds__(256) void k_banded_attention(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float pv = s[c][kt][r] * inv;
-          const _Float16 hi = (_Float16)pv;
-          ph[4 * kt + r] = hi;
-          pl[4 * kt + r] = (_Float16)(pv - (float)hi);
+          const _Float16 hi16 = (_Float16)pv;
+          ph[4 * kt + r] = hi16;
+          pl[4 * kt + r] = (_Float16)(pv - (float)hi16);
         }
       const int row = rb + 32 * c + 4 * lg;
 #pragma unroll
@@ -176,38 +260,37 @@ __global__ __launch_bounds__(256) void k_banded_attention(AttnArgs a) {
       uint16_t* orow = a.out + (seq0 + tq) * a.out_stride + hq * HD;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const uint32_t lo = (uint32_t)wasm_f2h(o[dt][0]) | ((uint32_t)wasm_f2h(o[dt][1]) << 16);
-        const uint32_t hi = (uint32_t)wasm_f2h(o[dt][2]) | ((uint32_t)wasm_f2h(o[dt][3]) << 16);
-        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = u2_t{lo, hi};
+        const float ov[4] = {o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
+        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = to_f16x4(ov);
       }
     }
   }
 }
 
-template <int HD, int NCH>
+template <int HD, int NCH, int NW>
 void launch_attn(pfhip_backend* b, const AttnArgs& a) {
-  constexpr int ROWS = 48 + 32 * NCH;
+  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;
   const size_t lds = (size_t)(ROWS * (HD + 8) + HD * (ROWS + 8)) * sizeof(_Float16);
   static bool attr_set = false;
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_banded_attention<HD, NCH>),
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_banded_attention<HD, NCH, NW>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
-  dim3 grid((a.T + QB - 1) / QB, a.Hkv, a.B);
+  dim3 grid((a.T + 16 * NW - 1) / (16 * NW), a.Hkv, a.B);
   ProfScope ps(b, "banded_attention");
-  hipLaunchKernelGGL((k_banded_attention<HD, NCH>), grid, dim3(256), lds, b->stream, a);
+  hipLaunchKernelGGL((k_banded_attention<HD, NCH, NW>), grid, dim3(64 * NW), lds, b->stream, a);
   PF_HIP(hipGetLastError());
 }
 
 template <int HD>
 void pick_nch(pfhip_backend* b, const AttnArgs& a) {
   const int need = (16 + 2 * a.window + 31) / 32;  // 32-key chunks per 16-query tile
-  if (need <= 1) return launch_attn<HD, 1>(b, a);
-  if (need <= 2) return launch_attn<HD, 2>(b, a);
-  if (need <= 3) return launch_attn<HD, 3>(b, a);
-  if (need <= 5) return launch_attn<HD, 5>(b, a);
-  return launch_attn<HD, 9>(b, a);
+  if (need <= 1) return launch_attn<HD, 1, 4>(b, a);
+  if (need <= 2) return launch_attn<HD, 2, 4>(b, a);
+  if (need <= 3) return launch_attn<HD, 3, 4>(b, a);
+  if (need <= 5) return launch_attn<HD, 5, 8>(b, a);
+  return launch_attn<HD, 9, 8>(b, a);
 }
 
 }  // namespace
@@ -215,7 +298,7 @@ void pick_nch(pfhip_backend* b, const AttnArgs& a) {
 void banded_attention(pfhip_backend* b, const AttnArgs& a) {
   PF_CHECK(a.head_dim == 64 || a.head_dim == 32, "banded_attention: head_dim must be 32 or 64");
   PF_CHECK(a.Hkv > 0 && a.Hq % a.Hkv == 0, "banded_attention: Hq must be a multiple of Hkv");
-  // 16 + 2W keys per 16-query tile must fit nine 32-key chunks (LDS: 92 KB)
+  // 16 + 2W keys per 16-query tile must fit nine 32-key chunks (LDS: 110 KB)
   PF_CHECK(a.window >= 0 && a.window <= 128, "banded_attention: window must be in [0, 128]");
   PF_CHECK(a.q && a.k && a.v && a.out, "banded_attention: null operand");
   PF_CHECK(a.q_stride % 8 == 0 && a.k_stride % 8 == 0 && a.v_stride % 8 == 0 && a.out_stride % 4 == 0,

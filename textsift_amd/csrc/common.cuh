@@ -48,6 +48,20 @@ __device__ __forceinline__ uint16_t wasm_f2h(float f) {
   return (uint16_t)(sign | ((mant24 + (1u << (shift - 1))) >> shift));
 }
 
+// True when the fp16 rounding of f involves none of the cases in which the
+// wasm helpers differ from the hardware: f is zero or |f| lies in
+// [2^-14, 65504] (no subnormal, overflow or NaN result). For such f,
+// wasm_f2h(f) is the hardware conversion and wasm_h2f of the result is the
+// hardware widening.
+__device__ __forceinline__ bool f16_plain(float f) {
+  const uint32_t a = __float_as_uint(f) & 0x7fffffffu;
+  return a == 0u || a - 0x38800000u <= 0x0EFFE000u;
+}
+
+// Hardware f32 -> fp16 (round to nearest even) and the fp16 round trip.
+__device__ __forceinline__ uint16_t hw_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ float round16(float f) { return (float)(_Float16)f; }
+
 // Hardware IEEE widen (used for MFMA operands; differs from wasm_h2f only on
 // fp16 subnormals).
 __device__ __forceinline__ float hw_h2f(uint16_t h) {

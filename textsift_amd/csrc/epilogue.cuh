@@ -1,0 +1,141 @@
+// epilogue.cuh — output stage shared by the int4 GEMM kernels.
+//
+// A lane holds 4 consecutive output columns n..n+3 of one output row (the
+// GEMMs are computed transposed). The conversions to fp16 follow the
+// reference (zig/math.zig:45-82) bit for bit; the cheap hardware conversion
+// is used where the two agree (f16_plain) and the exact software path only
+// for lanes where they may not.
+#pragma once
+#include "common.cuh"
+#include "pfhip_internal.h"
+
+namespace pf {
+
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u2_t pack4(const uint16_t hb[4]) {
+  return u2_t{(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+}
+
+// The exact (software) conversions, for the rare lanes the fast paths below
+// cannot take. Not inlined, so the epilogues that call them stay small
+// enough to unroll (their accumulators then stay in registers).
+__device__ __noinline__ u2_t to_f16x4_exact(f4_t v) {
+  uint16_t hb[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) hb[r] = wasm_f2h(v[r]);
+  return pack4(hb);
+}
+
+// rope_apply (zig/wasm_exports.zig:1460-1502) on one pair of fp16 values:
+// each product rounded to fp16, combined in f32, rounded again. c and s are
+// the table entries widened as the reference widens them.
+__device__ __forceinline__ void rope_pair_exact(uint16_t& ha, uint16_t& hb, float c, float s) {
+  const float a = wasm_h2f(ha), b = wasm_h2f(hb);
+  const float ac = wasm_h2f(wasm_f2h(a * c)), bs = wasm_h2f(wasm_f2h(b * s));
+  const float bc = wasm_h2f(wasm_f2h(b * c)), as_ = wasm_h2f(wasm_f2h(a * s));
+  ha = wasm_f2h(ac - bs);
+  hb = wasm_f2h(bc + as_);
+}
+
+__device__ __noinline__ u2_t rope_f16x4_exact(f4_t v, f2_t cs, f2_t sn) {
+  uint16_t hb[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) hb[r] = wasm_f2h(v[r]);
+  rope_pair_exact(hb[0], hb[1], cs[0], sn[0]);
+  rope_pair_exact(hb[2], hb[3], cs[1], sn[1]);
+  return pack4(hb);
+}
+
+// 4 f32 -> 4 fp16 as wasm_f2h rounds.
+__device__ __forceinline__ u2_t to_f16x4(const float v[4]) {
+  uint16_t hb[4];
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    hb[r] = hw_f2h(v[r]);
+    ok = ok && f16_plain(v[r]);
+  }
+  if (!ok) return to_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]});
+  return pack4(hb);
+}
+
+// fp16 output of v with the RoPE rotation of pairs (n, n+1), (n+2, n+3)
+// (cs, sn: the two pairs' table entries at the row's sequence position).
+__device__ __forceinline__ u2_t rope_f16x4(const float v[4], f2_t cs, f2_t sn) {
+  uint16_t hb[4];
+  bool ok = f16_plain(v[0]) && f16_plain(v[1]) && f16_plain(v[2]) && f16_plain(v[3]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float a = round16(v[2 * h]), b = round16(v[2 * h + 1]);
+    const float c = cs[h], s = sn[h];
+    const float p1 = a * c, p2 = b * s, p3 = b * c, p4 = a * s;
+    ok = ok && f16_plain(p1) && f16_plain(p2) && f16_plain(p3) && f16_plain(p4);
+    const float r0 = round16(p1) - round16(p2);
+    const float r1 = round16(p3) + round16(p4);
+    ok = ok && f16_plain(r0) && f16_plain(r1);
+    hb[2 * h] = hw_f2h(r0);
+    hb[2 * h + 1] = hw_f2h(r1);
+  }
+  if (!ok) return rope_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]}, cs, sn);
+  return pack4(hb);
+}
+
+// Writes v (bias already added) for output row orow, columns n..n+3.
+//   F32 / F16: out[orow][n..n+3]
+//   ROPE_F16: fp16 with RoPE on columns below rope_cols (head_dim 64)
+//   SWIGLU_*: (gate, up) interleaved columns -> out[orow][n/2 .. n/2+1]
+template <Epi EPI>
+__device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n, const float v[4]) {
+  if constexpr (EPI == Epi::F32) {
+    float* o = static_cast<float*>(p.out) + orow * p.ldo + n;
+    if (n + 3 < p.N) {
+      *reinterpret_cast<f4_t*>(o) = f4_t{v[0], v[1], v[2], v[3]};
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (n + r < p.N) o[r] = v[r];
+    }
+  } else if constexpr (EPI == Epi::F16 || EPI == Epi::ROPE_F16) {
+    u2_t hv;
+    if constexpr (EPI == Epi::ROPE_F16) {
+      if (n < p.rope_cols) {
+        const int pos = (int)(orow % (size_t)p.seq_len);
+        const int pidx = (n & 63) >> 1;
+        const f2_t cs = *reinterpret_cast<const f2_t*>(p.rope_cos + pos * 32 + pidx);
+        const f2_t sn = *reinterpret_cast<const f2_t*>(p.rope_sin + pos * 32 + pidx);
+        hv = rope_f16x4(v, cs, sn);
+      } else {
+        hv = to_f16x4(v);
+      }
+    } else {
+      hv = to_f16x4(v);
+    }
+    uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
+    if (n + 3 < p.N) {
+      *reinterpret_cast<u2_t*>(o) = hv;
+    } else {
+      const uint32_t w2[2] = {hv.x, hv.y};
+      for (int r = 0; r < 4; ++r)
+        if (n + r < p.N) o[r] = (uint16_t)(w2[r >> 1] >> (16 * (r & 1)));
+    }
+  } else {
+    const float g0 = swiglu_clamp(v[0], v[1]);
+    const float g1 = swiglu_clamp(v[2], v[3]);
+    const size_t oc = (size_t)(n >> 1);
+    if constexpr (EPI == Epi::SWIGLU_SPLIT) {
+      // f32 SwiGLU output (expert.ts keeps it f32) as hi/lo fp16 planes
+      uint16_t a0, a1, e0, e1;
+      split_hilo(g0, a0, e0);
+      split_hilo(g1, a1, e1);
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) =
+          (uint32_t)a0 | ((uint32_t)a1 << 16);
+      *reinterpret_cast<uint32_t*>(p.out_lo + orow * p.ldo + oc) = (uint32_t)e0 | ((uint32_t)e1 << 16);
+    } else {
+      uint32_t h = (uint32_t)hw_f2h(g0) | ((uint32_t)hw_f2h(g1) << 16);
+      if (!(f16_plain(g0) && f16_plain(g1))) h = to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) = h;
+    }
+  }
+}
+
+}  // namespace pf

@@ -82,8 +82,8 @@ struct pfhip_model {
   int cap_tokens = 0;
   // RoPE tables for one sequence length
   int rope_T = 0;
-  uint16_t* rope_cos = nullptr;
-  uint16_t* rope_sin = nullptr;
+  float* rope_cos = nullptr;  // fp16 table entries, widened as the reference widens them
+  float* rope_sin = nullptr;
   // host-API staging
   pfhip_buffer* ids_buf = nullptr;
   pfhip_buffer* mask_buf = nullptr;
@@ -152,6 +152,15 @@ uint16_t f32_to_fp16_host(float f) {
     if (++e >= 0x1fu) return (uint16_t)(sign | 0x7c00u);
   }
   return (uint16_t)(sign | (e << 10) | m10);
+}
+
+// fp16 bits -> f32 as zig/math.zig:45-52 widens (subnormals rebiased).
+float wasm_h2f_host(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16, rest = (uint32_t)h & 0x7fffu;
+  const uint32_t u = sign | (rest == 0u ? 0u : (rest << 13) + (112u << 23));
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
 }
 
 void build_rope_tables(const pfhip_model_config& c, int T, std::vector<uint16_t>& cs, std::vector<uint16_t>& sn) {
@@ -285,10 +294,15 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       hipFree(m->rope_sin);
       m->rope_cos = m->rope_sin = nullptr;
     }
-    PF_HIP(hipMalloc(&m->rope_cos, cs.size() * 2));
-    PF_HIP(hipMalloc(&m->rope_sin, sn.size() * 2));
-    PF_HIP(hipMemcpy(m->rope_cos, cs.data(), cs.size() * 2, hipMemcpyHostToDevice));
-    PF_HIP(hipMemcpy(m->rope_sin, sn.data(), sn.size() * 2, hipMemcpyHostToDevice));
+    std::vector<float> csf(cs.size()), snf(sn.size());
+    for (size_t i = 0; i < cs.size(); ++i) {
+      csf[i] = wasm_h2f_host(cs[i]);
+      snf[i] = wasm_h2f_host(sn[i]);
+    }
+    PF_HIP(hipMalloc(&m->rope_cos, csf.size() * 4));
+    PF_HIP(hipMalloc(&m->rope_sin, snf.size() * 4));
+    PF_HIP(hipMemcpy(m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice));
+    PF_HIP(hipMemcpy(m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice));
     m->rope_T = T;
   }
 

@@ -28,6 +28,7 @@
 //    built by the MoE routing kernels; weights are offset per expert and
 //    activation rows may be gathered through row_map.
 #include "common.cuh"
+#include "epilogue.cuh"
 #include "pfhip_internal.h"
 
 namespace pf {
@@ -250,63 +251,7 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bv[r];
-      if constexpr (EPI == Epi::F32) {
-        float* o = static_cast<float*>(p.out) + orow * p.ldo + n;
-        if (n + 3 < p.N) {
-          *reinterpret_cast<f4_t*>(o) = f4_t{v[0], v[1], v[2], v[3]};
-        } else {
-          for (int r = 0; r < 4; ++r)
-            if (n + r < p.N) o[r] = v[r];
-        }
-      } else if constexpr (EPI == Epi::F16 || EPI == Epi::ROPE_F16) {
-        uint16_t hb[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hb[r] = wasm_f2h(v[r]);
-        if constexpr (EPI == Epi::ROPE_F16) {
-          if (n < p.rope_cols) {
-            // rope_apply (zig/wasm_exports.zig:1460-1502) on the fp16 values:
-            // each product rounded to fp16, combined in f32, rounded again.
-            const int pos = (int)(orow % (size_t)p.seq_len);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const int pidx = ((n & 63) >> 1) + h;
-              const float c = wasm_h2f(p.rope_cos[pos * 32 + pidx]);
-              const float s = wasm_h2f(p.rope_sin[pos * 32 + pidx]);
-              const float a = wasm_h2f(hb[2 * h]), bb = wasm_h2f(hb[2 * h + 1]);
-              const float ac = wasm_h2f(wasm_f2h(a * c)), bs = wasm_h2f(wasm_f2h(bb * s));
-              const float bc = wasm_h2f(wasm_f2h(bb * c)), as_ = wasm_h2f(wasm_f2h(a * s));
-              hb[2 * h] = wasm_f2h(ac - bs);
-              hb[2 * h + 1] = wasm_f2h(bc + as_);
-            }
-          }
-        }
-        uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
-        if (n + 3 < p.N) {
-          *reinterpret_cast<u2_t*>(o) = u2_t{(uint32_t)hb[0] | ((uint32_t)hb[1] << 16),
-                                             (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
-        } else {
-          for (int r = 0; r < 4; ++r)
-            if (n + r < p.N) o[r] = hb[r];
-        }
-      } else {  // SwiGLU: (gate, up) interleaved columns -> glu column n/2
-        const float g0 = swiglu_clamp(v[0], v[1]);
-        const float g1 = swiglu_clamp(v[2], v[3]);
-        const size_t oc = (size_t)(n >> 1);
-        if constexpr (EPI == Epi::SWIGLU_SPLIT) {
-          // f32 SwiGLU output (expert.ts keeps it f32) as hi/lo fp16 planes
-          const _Float16 h0 = (_Float16)g0, h1 = (_Float16)g1;
-          const _Float16 e0 = (_Float16)(g0 - (float)h0), e1 = (_Float16)(g1 - (float)h1);
-          uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
-          uint16_t* ol = p.out_lo + orow * p.ldo + oc;
-          *reinterpret_cast<uint32_t*>(o) =
-              (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-          *reinterpret_cast<uint32_t*>(ol) =
-              (uint32_t)__builtin_bit_cast(uint16_t, e0) | ((uint32_t)__builtin_bit_cast(uint16_t, e1) << 16);
-        } else {
-          uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + oc;
-          *reinterpret_cast<uint32_t*>(o) = (uint32_t)wasm_f2h(g0) | ((uint32_t)wasm_f2h(g1) << 16);
-        }
-      }
+      store_out<EPI>(p, orow, n, v);
     }
   }
 }

@@ -4,6 +4,7 @@
 // MoE combine. Reference semantics: packages/textsift/src/zig/wasm_exports.zig
 // (line ranges cited per kernel).
 #include "common.cuh"
+#include "epilogue.cuh"
 #include "pfhip_internal.h"
 
 namespace pf {
@@ -13,67 +14,71 @@ namespace {
 constexpr int ROWS_PER_BLOCK = 4;  // one wave per row, 4 waves per block
 
 // ----------------------------------------------------------------------------
-// GatherBlockQuantized (embed_lookup_int4, :1523-1573): one wave per token
-// row. Lane l owns 16 B of packed nibbles (32 values = one quant block) for
-// lanes 0..D/32-1; the row's scales / zero-points are read once per lane.
+// GatherBlockQuantized (embed_lookup_int4, :1523-1573): one thread per 8
+// values of an output row (one dword of packed nibbles, 16 output bytes).
 // fp16((q - zp) * scale) is a single rounding of an exact product, so the
-// output is bit-identical to the reference.
+// output is bit-identical to the reference. Ids outside [0, V) give a zero row.
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
                                                const uint8_t* __restrict__ zp, const int32_t* __restrict__ ids,
                                                uint16_t* __restrict__ out, int T, int V, int D) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const int nb = D >> 5;
+  const int gpr = D >> 3;  // 8-value groups per row
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)T * gpr) return;
+  const int t = (int)(i / gpr), g = (int)(i % gpr);
+  const int nb = D >> 5, blk = g >> 2;
   const int id = ids[t];
-  uint16_t* o = out + (size_t)t * D;
-  for (int blk = lane; blk < nb; blk += 64) {
-    u4_t res[4] = {};
-    if (id >= 0 && id < V) {
-      const size_t row = (size_t)id;
-      const u4_t w = *reinterpret_cast<const u4_t*>(q + row * (D >> 1) + blk * 16);
-      const float sc = wasm_h2f(s[row * nb + blk]);
-      const uint8_t zb = zp[row * ((nb + 1) >> 1) + (blk >> 1)];
-      const int z = (blk & 1) ? (zb >> 4) : (zb & 0xF);
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+  u4_t res = {0u, 0u, 0u, 0u};
+  if (id >= 0 && id < V) {
+    const size_t row = (size_t)id;
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(q + row * (D >> 1) + g * 4);
+    const float sc = wasm_h2f(s[row * nb + blk]);
+    const uint8_t zb = zp[row * ((nb + 1) >> 1) + (blk >> 1)];
+    const int z = (blk & 1) ? (zb >> 4) : (zb & 0xF);
+    float v[8];
 #pragma unroll
-      for (int wi = 0; wi < 4; ++wi) {
-        uint32_t packed[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t byte = (words[wi] >> (8 * j)) & 0xFFu;
-          const float lo = (float)((int)(byte & 0xF) - z) * sc;
-          const float hi = (float)((int)(byte >> 4) - z) * sc;
-          packed[j] = (uint32_t)wasm_f2h(lo) | ((uint32_t)wasm_f2h(hi) << 16);
-        }
-        res[wi] = u4_t{packed[0], packed[1], packed[2], packed[3]};
-      }
-    }
-    u4_t* dst = reinterpret_cast<u4_t*>(o + blk * 32);
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi) dst[wi] = res[wi];
+    for (int j = 0; j < 8; ++j) v[j] = (float)((int)((w >> (4 * j)) & 0xFu) - z) * sc;
+    const u2_t a = to_f16x4(v), c = to_f16x4(v + 4);
+    res = u4_t{a.x, a.y, c.x, c.y};
   }
+  *reinterpret_cast<u4_t*>(out + (size_t)t * D + g * 8) = res;
 }
 
 // ----------------------------------------------------------------------------
-// RMSNorm family (:186-350). One wave per row, the row held in registers
-// (D <= 64 * 16). Widening is the reference's bit trick (wasm_h2f).
-constexpr int MAXPL = 16;  // elements per lane
+// RMSNorm family (:186-350). One wave per row; lane l holds elements
+// 4l + 256j .. +3 (8-byte loads), so D must be a multiple of 4 and <= 1024.
+// Widening is the reference's bit trick (wasm_h2f).
+constexpr int MAXJ = 4;  // 256-element slices per row
 
 // Output forms of a normalised row: fp16, f32, or the f32 value as hi/lo fp16 planes.
 enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_SPLIT = 2 };
 
+__device__ __forceinline__ void ld4_h2f(const uint16_t* p, float v[4]) {
+  const u2_t w = *reinterpret_cast<const u2_t*>(p);
+  v[0] = wasm_h2f((uint16_t)(w.x & 0xFFFFu));
+  v[1] = wasm_h2f((uint16_t)(w.x >> 16));
+  v[2] = wasm_h2f((uint16_t)(w.y & 0xFFFFu));
+  v[3] = wasm_h2f((uint16_t)(w.y >> 16));
+}
+
+__device__ __forceinline__ void h4_to_f(u2_t w, float v[4]) {
+  v[0] = wasm_h2f((uint16_t)(w.x & 0xFFFFu));
+  v[1] = wasm_h2f((uint16_t)(w.x >> 16));
+  v[2] = wasm_h2f((uint16_t)(w.y & 0xFFFFu));
+  v[3] = wasm_h2f((uint16_t)(w.y >> 16));
+}
+
 template <int MODE>
-__device__ __forceinline__ void put(void* out, uint16_t* out_lo, size_t i, float y) {
+__device__ __forceinline__ void put4(void* out, uint16_t* out_lo, size_t i, const float y[4]) {
   if constexpr (MODE == OUT_F32) {
-    static_cast<float*>(out)[i] = y;
+    *reinterpret_cast<f4_t*>(static_cast<float*>(out) + i) = f4_t{y[0], y[1], y[2], y[3]};
   } else if constexpr (MODE == OUT_F16) {
-    static_cast<uint16_t*>(out)[i] = wasm_f2h(y);
+    *reinterpret_cast<u2_t*>(static_cast<uint16_t*>(out) + i) = to_f16x4(y);
   } else {
-    uint16_t h, l;
-    split_hilo(y, h, l);
-    static_cast<uint16_t*>(out)[i] = h;
-    out_lo[i] = l;
+    uint16_t h[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) split_hilo(y[r], h[r], l[r]);
+    *reinterpret_cast<u2_t*>(static_cast<uint16_t*>(out) + i) = pack4(h);
+    *reinterpret_cast<u2_t*>(out_lo + i) = pack4(l);
   }
 }
 
@@ -84,22 +89,33 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
-  const uint16_t* xr = x + (size_t)t * D;
-  float v[MAXPL];
+  const size_t base = (size_t)t * D;
+  float v[MAXJ][4];
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < MAXPL; ++i) {
-    const int d = i * 64 + lane;
-    v[i] = d < D ? wasm_h2f(xr[d]) : 0.0f;
-    ss += v[i] * v[i];
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    if (d < D) {
+      ld4_h2f(x + base + d, v[j]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[j][r] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ss += v[j][r] * v[j][r];
   }
   ss = wave_sum(ss);
-  const float d_inv = 1.0f / (float)D;
-  const float inv_rms = 1.0f / sqrtf(ss * d_inv + eps);
+  const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
 #pragma unroll
-  for (int i = 0; i < MAXPL; ++i) {
-    const int d = i * 64 + lane;
-    if (d < D) put<MODE>(out, out_lo, (size_t)t * D + d, v[i] * inv_rms * wasm_h2f(g[d]));
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    if (d < D) {
+      float gm[4], y[4];
+      ld4_h2f(g + d, gm);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = v[j][r] * inv_rms * gm[r];
+      put4<MODE>(out, out_lo, base + d, y);
+    }
   }
 }
 
@@ -115,25 +131,38 @@ __global__ __launch_bounds__(256) void k_add_rms_norm(const uint16_t* __restrict
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
   const size_t base = (size_t)t * D;
-  uint16_t hs[MAXPL];
+  u2_t hs[MAXJ];
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < MAXPL; ++i) {
-    const int d = i * 64 + lane;
-    float sv = 0.0f;
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    hs[j] = u2_t{0u, 0u};
     if (d < D) {
-      sv = wasm_h2f(a[base + d]) + wasm_h2f(bb[base + d]);
-      hs[i] = wasm_f2h(sv);
-      sum_out[base + d] = hs[i];
+      float av[4], bv[4], sv[4];
+      ld4_h2f(a + base + d, av);
+      ld4_h2f(bb + base + d, bv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = av[r] + bv[r];
+        ss += sv[r] * sv[r];
+      }
+      hs[j] = to_f16x4(sv);
+      *reinterpret_cast<u2_t*>(sum_out + base + d) = hs[j];
     }
-    ss += sv * sv;
   }
   ss = wave_sum(ss);
   const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
 #pragma unroll
-  for (int i = 0; i < MAXPL; ++i) {
-    const int d = i * 64 + lane;
-    if (d < D) put<MODE>(norm_out, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(g[d]));
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    if (d < D) {
+      float hv[4], gm[4], y[4];
+      h4_to_f(hs[j], hv);
+      ld4_h2f(g + d, gm);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = hv[r] * inv_rms * gm[r];
+      put4<MODE>(norm_out, norm_lo, base + d, y);
+    }
   }
 }
 
@@ -208,13 +237,10 @@ __global__ void k_rope(uint16_t* qk, const uint16_t* cs, const uint16_t* sn, int
 // One thread per token replays the reference's insertion order exactly:
 // output sorted by logit descending, ties keep the lower expert id first.
 constexpr int MAXK = 8;
-__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int32_t* __restrict__ idx,
-                                                     float* __restrict__ w, int T, int E, int K, float wscale) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const float* x = logits + (size_t)t * E;
-  float V[MAXK];
-  int I[MAXK];
+// The reference's insertion top-k (sorted descending; an equal value never
+// displaces an earlier index) on one row, sequentially.
+template <int K>
+__device__ void topk_insertion(const float* x, int E, float* V, int* I) {
   for (int i = 0; i < K; ++i) { I[i] = i; V[i] = x[i]; }
   for (int s = 1; s < K; ++s)
     for (int j = s; j > 0 && V[j] > V[j - 1]; --j) {
@@ -232,14 +258,79 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
       }
     }
   }
-  float mx = V[0];
-  for (int c = 1; c < K; ++c) if (V[c] > mx) mx = V[c];
-  float e[MAXK], sum = 0.0f;
-  for (int c = 0; c < K; ++c) { e[c] = expf(V[c] - mx); sum += e[c]; }
-  const float inv = sum > 0.0f ? 1.0f / sum : 1.0f / (float)K;
-  for (int c = 0; c < K; ++c) {
-    idx[(size_t)t * K + c] = I[c];
-    w[(size_t)t * K + c] = (e[c] * inv) * wscale;
+}
+
+// One wave per token; lane l holds logits l, l+64, l+128, l+192. Without
+// NaNs the insertion top-k equals K rounds of "largest value, lowest index
+// among equal values", done as wave reductions; a row with a NaN takes the
+// sequential insertion path (whose comparisons NaN short-circuits).
+constexpr int TOPK_PL = 4;  // E <= 256
+template <int K>
+__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int32_t* __restrict__ idx,
+                                                     float* __restrict__ w, int T, int E, float wscale) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* x = logits + (size_t)t * E;
+  float xv[TOPK_PL];
+  bool live[TOPK_PL];
+  bool nan = false;
+#pragma unroll
+  for (int j = 0; j < TOPK_PL; ++j) {
+    const int c = lane + 64 * j;
+    live[j] = c < E;
+    xv[j] = live[j] ? x[c] : -INFINITY;
+    nan = nan || (live[j] && xv[j] != xv[j]);
+  }
+  float V[K];
+  int I[K];
+  if (__any(nan)) {
+    if (lane == 0) topk_insertion<K>(x, E, V, I);
+    // broadcast lane 0's result
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      V[k] = __shfl(V[k], 0, 64);
+      I[k] = __shfl(I[k], 0, 64);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < TOPK_PL; ++j) {
+        const int c = lane + 64 * j;
+        const bool take = live[j] & ((xv[j] > bv) | ((xv[j] == bv) & (c < bi)));
+        bv = take ? xv[j] : bv;
+        bi = take ? c : bi;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
+        bv = take ? ov : bv;
+        bi = take ? oi : bi;
+      }
+      V[k] = bv;
+      I[k] = bi;
+#pragma unroll
+      for (int j = 0; j < TOPK_PL; ++j) live[j] = live[j] & (lane + 64 * j != bi);
+    }
+  }
+  if (lane == 0) {
+    float mx = V[0];
+#pragma unroll
+    for (int c = 1; c < K; ++c) if (V[c] > mx) mx = V[c];
+    float e[K], sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < K; ++c) { e[c] = expf(V[c] - mx); sum += e[c]; }
+    const float inv = sum > 0.0f ? 1.0f / sum : 1.0f / (float)K;
+#pragma unroll
+    for (int c = 0; c < K; ++c) {
+      idx[(size_t)t * K + c] = I[c];
+      w[(size_t)t * K + c] = (e[c] * inv) * wscale;
+    }
   }
 }
 
@@ -250,87 +341,176 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 // expert.ts:125-145). Deterministic: no atomics anywhere.
 constexpr int RBLK = 256;  // tokens per counting block
 
-// counts[blk][e] = occurrences of e among the block's tokens. Thread e scans
-// the block's routing rows from LDS (broadcast reads).
-__global__ __launch_bounds__(256) void k_moe_count(const int32_t* __restrict__ idx, int32_t* __restrict__ counts,
-                                                   int T, int K, int E) {
-  __shared__ int32_t sidx[RBLK * MAXK];
+// Per-block expert bitmaps: bit t of bits[e][t / 32] is set when token t of
+// the block routes to expert e. OR is order-independent, so the bitmap (and
+// everything derived from it) is deterministic. Entries with an expert id
+// outside [0, E) are ignored.
+__device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx, uint32_t* bits, int t0, int nt,
+                                                 int K, int E) {
+  for (int i = threadIdx.x; i < E * (RBLK / 32); i += blockDim.x) bits[i] = 0u;
+  __syncthreads();
+  const int tl = threadIdx.x;
+  if (tl < nt)
+    for (int k = 0; k < K; ++k) {
+      const int e = idx[(size_t)(t0 + tl) * K + k];
+      if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * (RBLK / 32) + (tl >> 5)], 1u << (tl & 31));
+    }
+  __syncthreads();
+}
+
+// counts[blk][e] = tokens of block blk routed to expert e.
+__global__ __launch_bounds__(RBLK) void k_moe_count(const int32_t* __restrict__ idx, int32_t* __restrict__ counts,
+                                                    int T, int K, int E) {
+  __shared__ uint32_t bits[256 * (RBLK / 32)];
   const int blk = blockIdx.x;
   const int t0 = blk * RBLK;
-  const int nt = min(RBLK, T - t0);
-  for (int i = threadIdx.x; i < nt * K; i += blockDim.x) sidx[i] = idx[(size_t)t0 * K + i];
-  __syncthreads();
+  moe_block_bitmap(idx, bits, t0, min(RBLK, T - t0), K, E);
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int c = 0;
-    for (int i = 0; i < nt * K; ++i) c += sidx[i] == e;
+#pragma unroll
+    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[e * (RBLK / 32) + w]);
     counts[(size_t)blk * E + e] = c;
   }
 }
 
-// Single workgroup: expert offsets, per-(block, expert) offsets and the
+// One workgroup of 1024 threads: G = 1024 / E2 threads per expert (E2 = E
+// rounded up to a power of two), thread (j, e) owning a contiguous range of
+// blocks. Produces expert offsets, per-(block, expert) slot offsets and the
 // grouped-GEMM tile list (expert, row0, rows).
-__global__ __launch_bounds__(256) void k_moe_scan(const int32_t* __restrict__ counts, int32_t* __restrict__ blk_off,
-                                                  int32_t* __restrict__ expert_off, int32_t* __restrict__ tiles,
-                                                  int32_t* __restrict__ num_tiles, int nblk, int E, int tile_t) {
-  __shared__ int32_t tot[256];
-  __shared__ int32_t ntl[256];
-  const int e = threadIdx.x;
-  int total = 0;
-  if (e < E)
-    for (int b = 0; b < nblk; ++b) total += counts[(size_t)b * E + e];
-  tot[e] = e < E ? total : 0;
-  ntl[e] = e < E ? (total + tile_t - 1) / tile_t : 0;
-  __syncthreads();
-  if (e == 0) {  // sequential exclusive scans over <= 256 experts
-    int acc = 0, tacc = 0;
-    for (int i = 0; i < E; ++i) {
-      const int c = tot[i], n = ntl[i];
-      tot[i] = acc;
-      ntl[i] = tacc;
-      acc += c;
-      tacc += n;
+constexpr int SCAN_THREADS = 1024;
+__global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ blk_off,
+                                                           int32_t* __restrict__ expert_off,
+                                                           int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ num_tiles, int nblk, int E, int E2,
+                                                           int tile_t) {
+  __shared__ int32_t part[SCAN_THREADS];  // [j][e] partial sums, then exclusive prefixes over j
+  __shared__ int32_t tot[257], ntl[256];
+  if (threadIdx.x < 256) {
+    tot[threadIdx.x] = 0;
+    ntl[threadIdx.x] = 0;
+  }
+  const int G = SCAN_THREADS / E2;
+  const int e = threadIdx.x % E2, j = threadIdx.x / E2;
+  const int per = (nblk + G - 1) / G;
+  const int b0 = min(nblk, j * per), b1 = min(nblk, b0 + per);
+  int sum = 0;
+  if (e < E) {
+    int b = b0;
+    for (; b + 8 <= b1; b += 8) {  // independent loads in flight
+      int c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = counts[(size_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += c[u];
     }
-    expert_off[E] = acc;
-    *num_tiles = tacc;
+    for (; b < b1; ++b) sum += counts[(size_t)b * E + e];
+  }
+  part[j * E2 + e] = sum;
+  __syncthreads();
+  if (j == 0) {  // exclusive prefix over j, per expert; totals
+    int acc = 0;
+    for (int jj = 0; jj < G; ++jj) {
+      const int v = part[jj * E2 + e];
+      part[jj * E2 + e] = acc;
+      acc += v;
+    }
+    if (e < E) {
+      tot[e] = acc;
+      ntl[e] = (acc + tile_t - 1) / tile_t;
+    }
+  }
+  __syncthreads();
+  // exclusive scans over experts (E <= 256) by the first wave, 4 experts per lane
+  if (threadIdx.x < 64) {
+    const int l = threadIdx.x;
+    int c[4], n[4], cs = 0, ns = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      c[u] = tot[4 * l + u];
+      n[u] = ntl[4 * l + u];
+      cs += c[u];
+      ns += n[u];
+    }
+    int ci = cs, ni = ns;  // inclusive scan of lane sums
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int a = __shfl_up(ci, o, 64), bb = __shfl_up(ni, o, 64);
+      if (l >= o) {
+        ci += a;
+        ni += bb;
+      }
+    }
+    int ce = ci - cs, ne = ni - ns;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      tot[4 * l + u] = ce;
+      ntl[4 * l + u] = ne;
+      ce += c[u];
+      ne += n[u];
+    }
+    if (l == 63) {
+      tot[256] = ce;  // grand total
+      expert_off[E] = ce;
+      *num_tiles = ne;
+    }
   }
   __syncthreads();
   if (e < E) {
     const int base = tot[e];
-    expert_off[e] = base;
-    int run = base;
-    for (int b = 0; b < nblk; ++b) {
+    if (j == 0) expert_off[e] = base;
+    int run = base + part[j * E2 + e];
+    int b = b0;
+    for (; b + 8 <= b1; b += 8) {
+      int c[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) c[u] = counts[(size_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        blk_off[(size_t)(b + u) * E + e] = run;
+        run += c[u];
+      }
+    }
+    for (; b < b1; ++b) {
       blk_off[(size_t)b * E + e] = run;
       run += counts[(size_t)b * E + e];
     }
-    int tix = ntl[e];
-    for (int r = 0; r < total; r += tile_t, ++tix) {
-      tiles[tix * 4 + 0] = e;
-      tiles[tix * 4 + 1] = base + r;
-      tiles[tix * 4 + 2] = min(tile_t, total - r);
-      tiles[tix * 4 + 3] = 0;
+    if (j == 0) {
+      const int total = (e + 1 < E ? tot[e + 1] : tot[256]) - base;
+      int tix = ntl[e];
+      for (int r = 0; r < total; r += tile_t, ++tix) {
+        reinterpret_cast<int4*>(tiles)[tix] = int4{e, base + r, min(tile_t, total - r), 0};
+      }
     }
   }
 }
 
-// Slot assignment: thread e walks the block's tokens in order.
-__global__ __launch_bounds__(256) void k_moe_scatter(const int32_t* __restrict__ idx,
-                                                     const int32_t* __restrict__ blk_off,
-                                                     int32_t* __restrict__ slot_token, int32_t* __restrict__ slot_of,
-                                                     int T, int K, int E) {
-  __shared__ int32_t sidx[RBLK * MAXK];
+// Slot assignment: slot = blk_off[blk][e] + number of earlier tokens of the
+// block routed to e (a popcount over the block bitmap). Within an expert the
+// slots follow the token order (a token's K experts are distinct).
+__global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict__ idx,
+                                                      const int32_t* __restrict__ blk_off,
+                                                      int32_t* __restrict__ slot_token, int32_t* __restrict__ slot_of,
+                                                      int T, int K, int E) {
+  __shared__ uint32_t bits[256 * (RBLK / 32)];
   const int blk = blockIdx.x;
   const int t0 = blk * RBLK;
   const int nt = min(RBLK, T - t0);
-  for (int i = threadIdx.x; i < nt * K; i += blockDim.x) sidx[i] = idx[(size_t)t0 * K + i];
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int pos = blk_off[(size_t)blk * E + e];
-    for (int i = 0; i < nt * K; ++i)
-      if (sidx[i] == e) {
-        slot_token[pos] = t0 + i / K;
-        slot_of[(size_t)t0 * K + i] = pos;
-        ++pos;
-      }
+  moe_block_bitmap(idx, bits, t0, nt, K, E);
+  const int tl = threadIdx.x;
+  if (tl >= nt) return;
+  const int wl = tl >> 5;
+  const uint32_t below = (1u << (tl & 31)) - 1u;
+  for (int k = 0; k < K; ++k) {
+    const size_t i = (size_t)(t0 + tl) * K + k;
+    const int e = idx[i];
+    if ((unsigned)e >= (unsigned)E) continue;
+    const uint32_t* be = bits + e * (RBLK / 32);
+    int rank = __popc(be[wl] & below);
+    for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
+    const int pos = blk_off[(size_t)blk * E + e] + rank;
+    slot_token[pos] = t0 + tl;
+    slot_of[i] = pos;
   }
 }
 
@@ -367,31 +547,49 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
       int ts = sk[j]; sk[j] = sk[j - 1]; sk[j - 1] = ts;
     }
   const size_t base = (size_t)t * D;
-  uint16_t hs[MAXPL];
+  u2_t hs[MAXJ];
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < MAXPL; ++i) {
-    const int d = i * 64 + lane;
-    float hv = 0.0f;
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    hs[j] = u2_t{0u, 0u};
     if (d < D) {
-      float acc = 0.0f;
-      for (int k = 0; k < K; ++k) acc = fmaf(wk[k], y[(size_t)sk[k] * D + d], acc);
-      const uint16_t m = wasm_f2h(acc);
-      if (moe_out) moe_out[base + d] = m;
-      hs[i] = wasm_f2h(wasm_h2f(residual[base + d]) + wasm_h2f(m));
-      h_out[base + d] = hs[i];
-      hv = wasm_h2f(hs[i]);
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k = 0; k < K; ++k) {
+        const f4_t yv = *reinterpret_cast<const f4_t*>(y + (size_t)sk[k] * D + d);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], yv[r], acc[r]);
+      }
+      const u2_t m = to_f16x4(acc);
+      if (moe_out) *reinterpret_cast<u2_t*>(moe_out + base + d) = m;
+      float mv[4], rv[4], sv[4];
+      h4_to_f(m, mv);
+      ld4_h2f(residual + base + d, rv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sv[r] = rv[r] + mv[r];
+      hs[j] = to_f16x4(sv);
+      *reinterpret_cast<u2_t*>(h_out + base + d) = hs[j];
+      float hv[4];
+      h4_to_f(hs[j], hv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ss += hv[r] * hv[r];
     }
-    ss += hv * hv;
   }
   if constexpr (NMODE >= 0) {
     // the next block's rms_norm_fp16_to_f32 on the new residual row (:220-270)
     ss = wave_sum(ss);
     const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
 #pragma unroll
-    for (int i = 0; i < MAXPL; ++i) {
-      const int d = i * 64 + lane;
-      if (d < D) put<NMODE>(norm_hi, norm_lo, base + d, wasm_h2f(hs[i]) * inv_rms * wasm_h2f(gamma[d]));
+    for (int j = 0; j < MAXJ; ++j) {
+      const int d = 4 * lane + 256 * j;
+      if (d < D) {
+        float hv[4], gm[4], yv[4];
+        h4_to_f(hs[j], hv);
+        ld4_h2f(gamma + d, gm);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = hv[r] * inv_rms * gm[r];
+        put4<NMODE>(norm_hi, norm_lo, base + d, yv);
+      }
     }
   }
 }
@@ -482,18 +680,19 @@ unsigned grid1d(size_t n, int block = 256) {
 
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D) {
-  PF_CHECK(D % 32 == 0 && D / 32 <= 64 * 4, "embed_lookup: D must be a multiple of 32");
-  PF_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0 && (D / 2) % 16 == 0,
-           "embed_lookup: table and output must be 16-byte aligned");
+  PF_CHECK(D > 0 && D % 32 == 0, "embed_lookup: D must be a multiple of 32");
+  PF_CHECK(((uintptr_t)q & 3) == 0 && ((uintptr_t)out & 15) == 0,
+           "embed_lookup: table must be 4-byte and output 16-byte aligned");
   if (T <= 0) return;
+  const size_t n = (size_t)T * (D / 8);
   ProfScope ps(b, "embed_lookup_int4");
-  hipLaunchKernelGGL(k_embed, dim3((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK), dim3(256), 0, b->stream, q, s, zp,
-                     ids, out, T, V, D);
+  hipLaunchKernelGGL(k_embed, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, b->stream, q, s, zp, ids, out, T, V,
+                     D);
   PF_HIP(hipGetLastError());
 }
 
 void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* out, int T, int D, float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "rms_norm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm");
   hipLaunchKernelGGL(k_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
@@ -501,7 +700,7 @@ void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16
 }
 
 void rms_norm_f32(pfhip_backend* b, const uint16_t* x, const uint16_t* g, float* out, int T, int D, float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "rms_norm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm_fp16_to_f32");
   hipLaunchKernelGGL(k_rms_norm<OUT_F32>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
@@ -510,7 +709,7 @@ void rms_norm_f32(pfhip_backend* b, const uint16_t* x, const uint16_t* g, float*
 
 void rms_norm_split(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* hi, uint16_t* lo, int T, int D,
                     float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "rms_norm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "rms_norm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm_split");
   hipLaunchKernelGGL(k_rms_norm<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, hi, lo, T, D, eps);
@@ -519,7 +718,7 @@ void rms_norm_split(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint
 
 void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
                       float* norm_out, int T, int D, float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "add_rmsnorm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "add_rmsnorm_fp16_to_f32");
   hipLaunchKernelGGL(k_add_rms_norm<OUT_F32>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out,
@@ -529,7 +728,7 @@ void add_rms_norm_f32(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, c
 
 void add_rms_norm_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g, uint16_t* sum_out,
                       uint16_t* norm_out, int T, int D, float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "add_rmsnorm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "add_rmsnorm_f16");
   hipLaunchKernelGGL(k_add_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out,
@@ -539,7 +738,7 @@ void add_rms_norm_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, c
 
 void add_rms_norm_split(pfhip_backend* b, const uint16_t* a, const uint16_t* bb, const uint16_t* g,
                         uint16_t* sum_out, uint16_t* hi, uint16_t* lo, int T, int D, float eps) {
-  PF_CHECK(D > 0 && D <= 64 * MAXPL, "add_rmsnorm: D out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "add_rmsnorm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "add_rmsnorm_split");
   hipLaunchKernelGGL(k_add_rms_norm<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, a, bb, g, sum_out, hi,
@@ -603,8 +802,16 @@ void rope_apply(pfhip_backend* b, uint16_t* qk, const uint16_t* c, const uint16_
 void router_topk(pfhip_backend* b, const float* logits, int32_t* idx, float* w, int T, int E, int K, float wscale) {
   PF_CHECK(K >= 1 && K <= MAXK && K <= E, "router_topk: need 1 <= K <= min(8, E)");
   if (T <= 0) return;
+  PF_CHECK(E <= 64 * TOPK_PL, "router_topk: E must be at most 256");
   ProfScope ps(b, "router_topk");
-  hipLaunchKernelGGL(k_router_topk, dim3((T + 255) / 256), dim3(256), 0, b->stream, logits, idx, w, T, E, K, wscale);
+  const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  switch (K) {
+#define PF_TOPK_CASE(k) \
+  case k: hipLaunchKernelGGL(k_router_topk<k>, grid, dim3(256), 0, b->stream, logits, idx, w, T, E, wscale); break;
+    PF_TOPK_CASE(1) PF_TOPK_CASE(2) PF_TOPK_CASE(3) PF_TOPK_CASE(4)
+    PF_TOPK_CASE(5) PF_TOPK_CASE(6) PF_TOPK_CASE(7) PF_TOPK_CASE(8)
+#undef PF_TOPK_CASE
+  }
   PF_HIP(hipGetLastError());
 }
 
@@ -645,8 +852,10 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
   }
   {
     ProfScope ps(b, "moe_scan");
-    hipLaunchKernelGGL(k_moe_scan, dim3(1), dim3(256), 0, b->stream, m.counts, m.blk_off, m.expert_off, m.tiles,
-                       m.num_tiles, nblk, E, m.tile_t);
+    int E2 = 1;
+    while (E2 < E) E2 <<= 1;
+    hipLaunchKernelGGL(k_moe_scan, dim3(1), dim3(SCAN_THREADS), 0, b->stream, m.counts, m.blk_off, m.expert_off,
+                       m.tiles, m.num_tiles, nblk, E, E2, m.tile_t);
     PF_HIP(hipGetLastError());
   }
   {
@@ -659,7 +868,7 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
 
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                  const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D) {
-  PF_CHECK(D <= 64 * MAXPL && K <= MAXK, "moe_combine: shape out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine");
   hipLaunchKernelGGL(k_moe_combine<-1>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
@@ -670,7 +879,7 @@ void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                       const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps) {
-  PF_CHECK(D <= 64 * MAXPL && K <= MAXK, "moe_combine: shape out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine_norm");
   if (norm_lo)

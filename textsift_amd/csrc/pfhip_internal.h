@@ -109,8 +109,8 @@ struct GemmArgs {
   const int32_t* num_tiles = nullptr;  // device scalar
   int max_tiles = 0;
   // RoPE epilogue
-  const uint16_t* rope_cos = nullptr;  // [seq_len][head_dim/2] fp16
-  const uint16_t* rope_sin = nullptr;
+  const float* rope_cos = nullptr;  // [seq_len][head_dim/2]: fp16 table entries widened as
+  const float* rope_sin = nullptr;  // wasm_h2f widens them (zig/math.zig:45-52)
   int seq_len = 0;
   int rope_cols = 0;                   // columns [0, rope_cols) are rotated
 };
