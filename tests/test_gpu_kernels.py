@@ -49,6 +49,28 @@ def run(be, name, inputs, out_bytes, pushb, out_init=None, out_index=None):
     return data
 
 
+# ---------------------------------------------------------------- fast math helpers
+
+def probe(be, which, lo, hi):
+    init = np.array([0, 0xFFFFFFFF, 0], np.uint32)
+    return run(be, "probe_fast_math", [], 12, u32s(which, lo, hi), out_init=init).view(np.uint32)
+
+
+def test_div_one_plus_exhaustive(be):
+    """e / (1 + e) by reciprocal + Newton-Raphson + remainder correction is
+    bit-identical to IEEE division for every f32 e in [0, 1]."""
+    out = probe(be, 0, 0, 0x3F800001)
+    assert out[0] == 0, f"{out[0]} mismatches, first at 0x{out[1]:08x}"
+
+
+def test_exp_approx_fast_exhaustive(be):
+    """exp_approx_fast == exp_approx for every f32 x <= 0 except where
+    floor(x log2 e) = -127 (both below 2^-126 there)."""
+    out = probe(be, 1, 0, 0x7F800000)
+    assert out[0] == 0, f"{out[0]} mismatches, first at 0x{out[1]:08x}"
+    print(f"differing inputs in the documented edge region: {out[2]}")
+
+
 # ---------------------------------------------------------------- MFMA operand layout
 
 def test_mfma_16x16x32_f16_layout(be):

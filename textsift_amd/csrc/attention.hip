@@ -31,24 +31,11 @@ namespace pf {
 
 namespace {
 
-// exp_approx with the final scaling done by ldexp. The two differ only when
-// floor(x log2 e) = -127 (x < -87.3): exp_approx returns 0 there, this a
-// value below 2^-126. Such a term is below 2^-126 of the row maximum's (which
-// is 1), so it leaves the f32 row sum unchanged and its probability rounds
-// to fp16 zero in both hi and lo: the attention output is identical.
-__device__ __forceinline__ float exp_softmax(float x) {
-  const float LOG2_E = 1.44269504088896340736f;
-  const float y = fmaxf(x, -88.0f) * LOG2_E;
-  const float fl = floorf(y);
-  const float frac = y - fl;
-  float poly = fmaf(0.001333355f, frac, 0.009679494f);
-  poly = fmaf(poly, frac, 0.055053319f);
-  poly = fmaf(poly, frac, 0.240226522f);
-  poly = fmaf(poly, frac, 0.693154774f);
-  poly = fmaf(poly, frac, 1.000000012f);
-  return __builtin_amdgcn_ldexpf(poly, (int)fl);
-}
-
+// The softmax uses exp_approx_fast where the reference uses expApprox. They
+// differ only when floor(x log2 e) = -127 (x < -87.3): such a term is below
+// 2^-126 of the row maximum's (which is 1), so it leaves the f32 row sum
+// unchanged and its probability rounds to fp16 zero in both hi and lo: the
+// attention output is identical.
 __device__ __forceinline__ int wave_min_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
@@ -202,7 +189,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float e = exp_softmax(s[c][kt][r] - m);
+            const float e = exp_approx_fast(s[c][kt][r] - m);
             s[c][kt][r] = e;
             l += e;
           }
@@ -214,7 +201,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
             const float sv = s[c][kt][r];
             const float x = sv - m;
             const int off = 32 * c + 16 * kt + 4 * lg + r;
-            float e = off >= tail ? expf(x) : exp_softmax(x);
+            float e = off >= tail ? expf(x) : exp_approx_fast(x);
             e = (sv != sv) ? 0.0f : e;
             s[c][kt][r] = e;
             l += e;
@@ -224,7 +211,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
     }
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    l += n_keys < vec_end ? exp_softmax(sink - m) : expf(sink - m);
+    l += n_keys < vec_end ? exp_approx_fast(sink - m) : expf(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 
     // ---- pass 3: O^T = V^T . P^T with P normalised, as fp16 hi + lo
@@ -238,7 +225,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pv = s[c][kt][r] * inv;
+          const float pv = f32_fence(s[c][kt][r] * inv);  // split the f32 probability
           const _Float16 hi16 = (_Float16)pv;
           ph[4 * kt + r] = hi16;
           pl[4 * kt + r] = (_Float16)(pv - (float)hi16);

@@ -30,7 +30,17 @@ __device__ __forceinline__ float wasm_h2f(uint16_t h) {
 
 // f32 -> fp16 bits as zig/math.zig:54-82: RNE for normal results (what the
 // hardware conversion does), round-half-up for subnormal results.
+// The compiler may fuse "round an f32 product or sum to fp16" into one
+// v_fma_mix*_f16, which rounds the exact result once instead of rounding it
+// to f32 first. f32_fence makes the value an opaque f32 so the conversions
+// below round exactly the f32 value they are given.
+__device__ __forceinline__ float f32_fence(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+
 __device__ __forceinline__ uint16_t wasm_f2h(float f) {
+  f = f32_fence(f);
   const float a = fabsf(f);
   if (a >= 6.103515625e-05f || !(a == a)) {
     _Float16 h = (_Float16)f;
@@ -58,9 +68,14 @@ __device__ __forceinline__ bool f16_plain(float f) {
   return a == 0u || a - 0x38800000u <= 0x0EFFE000u;
 }
 
-// Hardware f32 -> fp16 (round to nearest even) and the fp16 round trip.
-__device__ __forceinline__ uint16_t hw_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-__device__ __forceinline__ float round16(float f) { return (float)(_Float16)f; }
+// Hardware f32 -> fp16 (round to nearest even) and the fp16 round trip, of
+// the f32 value given (fenced, see f32_fence).
+__device__ __forceinline__ uint16_t hw_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f32_fence(f)); }
+__device__ __forceinline__ float round16(float f) { return (float)(_Float16)f32_fence(f); }
+// The fp16 round trip of a value the caller knows to be exact in f32 (such
+// as a product of two fp16 values): a fused single rounding is then the
+// same, so no fence.
+__device__ __forceinline__ float round16_exact(float f) { return (float)(_Float16)f; }
 
 // Hardware IEEE widen (used for MFMA operands; differs from wasm_h2f only on
 // fp16 subnormals).
@@ -71,6 +86,7 @@ __device__ __forceinline__ float hw_h2f(uint16_t h) {
 // f32 -> exact (hi, lo) fp16 pair: hi = fp16(v), lo = fp16(v - hi); hi + lo
 // carries 22 significant bits of v (the form SPLIT GEMM inputs take).
 __device__ __forceinline__ void split_hilo(float v, uint16_t& hi, uint16_t& lo) {
+  v = f32_fence(v);
   const _Float16 h = (_Float16)v;
   const _Float16 l = (_Float16)(v - (float)h);
   hi = __builtin_bit_cast(uint16_t, h);
@@ -96,21 +112,64 @@ __device__ __forceinline__ float exp_approx(float x) {
   return poly * scale;
 }
 
-// sigmoidF32x4 (zig/wasm_exports.zig:843-853), one lane.
+// exp_approx with the final scaling done by ldexp. The two give the same
+// value unless floor(x log2 e) = -127 (x < -87.3), where exp_approx returns
+// 0 and this a value below 2^-126 (tests/test_gpu_kernels.py checks every
+// other f32 x <= 0 exhaustively). Callers use it where such a difference
+// cannot reach their output (see each call site).
+__device__ __forceinline__ float exp_approx_fast(float x) {
+  const float LOG2_E = 1.44269504088896340736f;
+  const float y = fmaxf(x, -88.0f) * LOG2_E;
+  const float fl = floorf(y);
+  const float frac = y - fl;  // fl is an integer of magnitude <= 127: y - (float)(int)fl
+  float poly = fmaf(0.001333355f, frac, 0.009679494f);
+  poly = fmaf(poly, frac, 0.055053319f);
+  poly = fmaf(poly, frac, 0.240226522f);
+  poly = fmaf(poly, frac, 0.693154774f);
+  poly = fmaf(poly, frac, 1.000000012f);
+  return __builtin_amdgcn_ldexpf(poly, (int)fl);
+}
+
+// e / (1 + e) for e in [0, 1], correctly rounded: hardware reciprocal of
+// b = 1 + e refined by one Newton-Raphson step, then one remainder
+// correction of the quotient (Markstein 1990; Cornea-Hasegan, Golliver and
+// Markstein 1999). tests/test_gpu_kernels.py compares it with IEEE division
+// for every f32 e in [0, 1].
+__device__ __forceinline__ float div_one_plus(float e) {
+  const float b = 1.0f + e;
+  float r = __builtin_amdgcn_rcpf(b);
+  r = fmaf(fmaf(-b, r, 1.0f), r, r);
+  const float q = e * r;
+  return fmaf(fmaf(-b, q, e), r, q);
+}
+
+// sigmoidF32x4 (zig/wasm_exports.zig:843-853), one lane:
+// neg_abs = min(x, 0) - max(x, 0) (= -|x|), e = expApprox(neg_abs),
+// sig_neg = e / (1 + e), x >= 0 ? 1 - sig_neg : sig_neg.
 __device__ __forceinline__ float sigmoid_approx(float x) {
-  float neg_abs = fminf(x, 0.0f) - fmaxf(x, 0.0f);
-  float e = exp_approx(neg_abs);
-  float sig_neg = e / (1.0f + e);
+  const float sig_neg = div_one_plus(exp_approx(-fabsf(x)));
+  return x >= 0.0f ? 1.0f - sig_neg : sig_neg;
+}
+// The same with exp_approx_fast: e differs only for |x| > 87.3, where
+// e < 2^-126, 1 - sig_neg = 1 exactly and sig_neg < 2^-126 either way.
+__device__ __forceinline__ float sigmoid_approx_fast(float x) {
+  const float sig_neg = div_one_plus(exp_approx_fast(-fabsf(x)));
   return x >= 0.0f ? 1.0f - sig_neg : sig_neg;
 }
 
 // SwiGLU with clamp (zig/wasm_exports.zig:855-903 vector path).
 __device__ __forceinline__ float swiglu_clamp(float gate_raw, float up_raw) {
-  float gate = fminf(gate_raw, 7.0f);
-  float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
-  float scaled = gate * 1.702f;
-  float glu = gate * sigmoid_approx(scaled);
-  return (up + 1.0f) * glu;
+  const float gate = fminf(gate_raw, 7.0f);
+  const float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
+  return (up + 1.0f) * (gate * sigmoid_approx(gate * 1.702f));
+}
+// The same for outputs stored as fp16 or hi/lo fp16: where the fast
+// sigmoid differs (gate < -51.3) the result is below 2^-120 in magnitude and
+// both round to a zero fp16 (hi and lo).
+__device__ __forceinline__ float swiglu_clamp_fast(float gate_raw, float up_raw) {
+  const float gate = fminf(gate_raw, 7.0f);
+  const float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
+  return (up + 1.0f) * (gate * sigmoid_approx_fast(gate * 1.702f));
 }
 
 // v_mfma_f32_16x16x32_f16 (gfx950). Operand layout (lane l, i = l / 16):

@@ -29,7 +29,10 @@ __device__ __noinline__ u2_t to_f16x4_exact(f4_t v) {
 
 // rope_apply (zig/wasm_exports.zig:1460-1502) on one pair of fp16 values:
 // each product rounded to fp16, combined in f32, rounded again. c and s are
-// the table entries widened as the reference widens them.
+// the table entries widened as the reference widens them. Both factors of
+// every product are fp16 values (<= 11 significant bits), so the product is
+// exact in f32 and rounding it once to fp16 (as v_fma_mixlo_f16 does when the
+// compiler fuses the conversion) equals rounding it to f32 first.
 __device__ __forceinline__ void rope_pair_exact(uint16_t& ha, uint16_t& hb, float c, float s) {
   const float a = wasm_h2f(ha), b = wasm_h2f(hb);
   const float ac = wasm_h2f(wasm_f2h(a * c)), bs = wasm_h2f(wasm_f2h(b * s));
@@ -54,7 +57,7 @@ __device__ __forceinline__ u2_t to_f16x4(const float v[4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     hb[r] = hw_f2h(v[r]);
-    ok = ok && f16_plain(v[r]);
+    ok &= f16_plain(v[r]);  // bitwise: no branch per test
   }
   if (!ok) return to_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]});
   return pack4(hb);
@@ -62,31 +65,39 @@ __device__ __forceinline__ u2_t to_f16x4(const float v[4]) {
 
 // fp16 output of v with the RoPE rotation of pairs (n, n+1), (n+2, n+3)
 // (cs, sn: the two pairs' table entries at the row's sequence position).
+// The fast path needs every value that gets rounded to fp16 to lie in
+// [2^-14, 65504] in magnitude (a stricter test than f16_plain: exact zeros,
+// rare here, also take the exact path); one min/max over all 16 of them.
 __device__ __forceinline__ u2_t rope_f16x4(const float v[4], f2_t cs, f2_t sn) {
   uint16_t hb[4];
-  bool ok = f16_plain(v[0]) && f16_plain(v[1]) && f16_plain(v[2]) && f16_plain(v[3]);
+  float lo = fminf(fminf(fabsf(v[0]), fabsf(v[1])), fminf(fabsf(v[2]), fabsf(v[3])));
+  float hi = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float a = round16(v[2 * h]), b = round16(v[2 * h + 1]);
     const float c = cs[h], s = sn[h];
     const float p1 = a * c, p2 = b * s, p3 = b * c, p4 = a * s;
-    ok = ok && f16_plain(p1) && f16_plain(p2) && f16_plain(p3) && f16_plain(p4);
-    const float r0 = round16(p1) - round16(p2);
-    const float r1 = round16(p3) + round16(p4);
-    ok = ok && f16_plain(r0) && f16_plain(r1);
+    lo = fminf(lo, fminf(fminf(fabsf(p1), fabsf(p2)), fminf(fabsf(p3), fabsf(p4))));
+    hi = fmaxf(hi, fmaxf(fmaxf(fabsf(p1), fabsf(p2)), fmaxf(fabsf(p3), fabsf(p4))));
+    const float r0 = round16_exact(p1) - round16_exact(p2);  // fp16 x fp16: exact products
+    const float r1 = round16_exact(p3) + round16_exact(p4);
+    lo = fminf(lo, fminf(fabsf(r0), fabsf(r1)));
+    hi = fmaxf(hi, fmaxf(fabsf(r0), fabsf(r1)));
     hb[2 * h] = hw_f2h(r0);
     hb[2 * h + 1] = hw_f2h(r1);
   }
-  if (!ok) return rope_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]}, cs, sn);
+  // NaN anywhere makes both comparisons false
+  if (!(lo >= 6.103515625e-05f && hi <= 65504.0f)) return rope_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]}, cs, sn);
   return pack4(hb);
 }
 
 // Writes v (bias already added) for output row orow, columns n..n+3.
 //   F32 / F16: out[orow][n..n+3]
-//   ROPE_F16: fp16 with RoPE on columns below rope_cols (head_dim 64)
+//   ROPE_F16: fp16 with RoPE on columns below rope_cols (head_dim 64);
+//             pos = orow % seq_len (the row's position in its sequence)
 //   SWIGLU_*: (gate, up) interleaved columns -> out[orow][n/2 .. n/2+1]
 template <Epi EPI>
-__device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n, const float v[4]) {
+__device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n, const float v[4], int pos = 0) {
   if constexpr (EPI == Epi::F32) {
     float* o = static_cast<float*>(p.out) + orow * p.ldo + n;
     if (n + 3 < p.N) {
@@ -99,7 +110,6 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
     u2_t hv;
     if constexpr (EPI == Epi::ROPE_F16) {
       if (n < p.rope_cols) {
-        const int pos = (int)(orow % (size_t)p.seq_len);
         const int pidx = (n & 63) >> 1;
         const f2_t cs = *reinterpret_cast<const f2_t*>(p.rope_cos + pos * 32 + pidx);
         const f2_t sn = *reinterpret_cast<const f2_t*>(p.rope_sin + pos * 32 + pidx);
@@ -119,8 +129,8 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
         if (n + r < p.N) o[r] = (uint16_t)(w2[r >> 1] >> (16 * (r & 1)));
     }
   } else {
-    const float g0 = swiglu_clamp(v[0], v[1]);
-    const float g1 = swiglu_clamp(v[2], v[3]);
+    const float g0 = swiglu_clamp_fast(v[0], v[1]);
+    const float g1 = swiglu_clamp_fast(v[2], v[3]);
     const size_t oc = (size_t)(n >> 1);
     if constexpr (EPI == Epi::SWIGLU_SPLIT) {
       // f32 SwiGLU output (expert.ts keeps it f32) as hi/lo fp16 planes
@@ -132,7 +142,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
       *reinterpret_cast<uint32_t*>(p.out_lo + orow * p.ldo + oc) = (uint32_t)e0 | ((uint32_t)e1 << 16);
     } else {
       uint32_t h = (uint32_t)hw_f2h(g0) | ((uint32_t)hw_f2h(g1) << 16);
-      if (!(f16_plain(g0) && f16_plain(g1))) h = to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
+      if (!(f16_plain(g0) & f16_plain(g1))) h = to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
       *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) = h;
     }
   }

@@ -251,7 +251,9 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] + bv[r];
-      store_out<EPI>(p, orow, n, v);
+      int pos = 0;
+      if constexpr (EPI == Epi::ROPE_F16) pos = (int)((uint32_t)orow % (uint32_t)p.seq_len);  // rows < 2^31
+      store_out<EPI>(p, orow, n, v, pos);
     }
   }
 }
@@ -297,6 +299,7 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
   if (epi == Epi::ROPE_F16)
     PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
              "gemm_int4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
+  if (epi == Epi::ROPE_F16) PF_CHECK(!grouped && (long)a.M < (1L << 31), "RoPE epilogue: dense rows below 2^31");
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_int4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_int4: M must be non-negative");
   const bool split = xk == XKind::SPLIT;

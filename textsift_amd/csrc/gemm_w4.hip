@@ -19,10 +19,11 @@
 //  * K is permuted inside each 128-wide chunk: MFMA step j (0..3) takes the
 //    8 values K = 32*lg + 8*j .. +7 from lane group lg. The activation
 //    operand uses the same permutation, so the dot product is unchanged.
-//  * Weights are repacked once (w4_repack): each dword holds k0,k2,k4,k6 in
-//    its low half's nibbles and k1,k3,k5,k7 in its high half's, so one
-//    shift + and_or per pair produces (1024 + q) as packed fp16 in natural
-//    k order; one packed add subtracts (1024 + zp) exactly and one packed
+//  * Weights are repacked once (w4_repack): byte b of each dword holds k = b
+//    in its low nibble and k = b + 4 in its high nibble. Two masks (one
+//    shift) put the 8 values in bytes, and one v_perm_b32 per pair places two
+//    of them under 0x64 exponent bytes: (1024 + q) as packed fp16, in natural
+//    k order. One packed add subtracts (1024 + zp) exactly and one packed
 //    multiply applies the scale (the only rounding).
 //  * Activations are the shared operand: the workgroup's BT x 128 chunk is
 //    copied HBM -> LDS with global_load_lds_dwordx4 (no register staging),
@@ -59,10 +60,13 @@ __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(
 // One repacked dword (8 nibbles) -> fp16 (q - zp) * scale for k = 0..7.
 // off = (-(1024 + zp), -(1024 + zp)), sc = (scale, scale).
 __device__ __forceinline__ h8_t dequant_fold(uint32_t w, h2_t off, h2_t sc) {
-  const uint32_t p0 = (w & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p1 = ((w >> 4) & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p2 = ((w >> 8) & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p3 = ((w >> 12) & 0x000F000Fu) | 0x64006400u;
+  const uint32_t lo = w & 0x0F0F0F0Fu;          // k0 k1 k2 k3 (one per byte)
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // k4 k5 k6 k7
+  const uint32_t M = 0x64646464u;               // exponent bytes of 1024
+  const uint32_t p0 = __builtin_amdgcn_perm(M, lo, 0x04010400u);  // (1024 + k0, 1024 + k1)
+  const uint32_t p1 = __builtin_amdgcn_perm(M, lo, 0x04030402u);
+  const uint32_t p2 = __builtin_amdgcn_perm(M, hi, 0x04010400u);
+  const uint32_t p3 = __builtin_amdgcn_perm(M, hi, 0x04030402u);
   const h2_t d0 = (__builtin_bit_cast(h2_t, p0) + off) * sc;
   const h2_t d1 = (__builtin_bit_cast(h2_t, p1) + off) * sc;
   const h2_t d2 = (__builtin_bit_cast(h2_t, p2) + off) * sc;
@@ -227,7 +231,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = acc[f][tj][r] + bv[r];
-      store_out<EPI>(p, orow, n, v);
+      int pos = 0;
+      if constexpr (EPI == Epi::ROPE_F16) pos = (int)((uint32_t)orow % (uint32_t)p.seq_len);  // rows < 2^31
+      store_out<EPI>(p, orow, n, v, pos);
     }
   }
 }
@@ -272,18 +278,17 @@ void dispatch_grouped(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped
 
 // ---------------------------------------------------------------- weight prep
 
-// MatMulNBits bytes [G][N][K/2] (low nibble = even k) -> repacked dwords:
-// per 8 values, k0,k2,k4,k6 in nibbles 0-3 and k1,k3,k5,k7 in nibbles 4-7.
+// MatMulNBits bytes [G][N][K/2] (nibble k at bits 4k of the dword of 8
+// values) -> repacked dwords: value k at bits 8k (k < 4) or 8(k-4)+4.
 __global__ void k_w4_repack(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const uint32_t w = src[i];
   uint32_t r = 0;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const uint32_t byte = (w >> (8 * b)) & 0xFFu;
-    r |= (byte & 0xFu) << (4 * b);          // k = 2b   -> low half
-    r |= (byte >> 4) << (16 + 4 * b);       // k = 2b+1 -> high half
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t q = (w >> (4 * k)) & 0xFu;
+    r |= q << (k < 4 ? 8 * k : 8 * (k - 4) + 4);
   }
   dst[i] = r;
 }
@@ -323,6 +328,7 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   if (epi == Epi::ROPE_F16)
     PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
              "gemm_w4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
+  if (epi == Epi::ROPE_F16) PF_CHECK(!grouped && (long)a.M < (1L << 31), "RoPE epilogue: dense rows below 2^31");
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_w4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_w4: M must be non-negative");
   PF_CHECK(xk == XKind::F16, "gemm_w4: activations must be one fp16 plane");

@@ -676,7 +676,65 @@ unsigned grid1d(size_t n, int block = 256) {
   return (unsigned)(g ? g : 1);
 }
 
+// ----------------------------------------------------------------------------
+// Test probes. Each walks the f32 bit patterns [lo, hi) and counts the inputs
+// where a fast routine and the formulation it replaces disagree bit-wise:
+// out[0] = mismatches, out[1] = smallest mismatching pattern (init 0xFFFFFFFF),
+// out[2] = inputs outside the routine's stated domain that differ.
+__global__ void k_probe_div_one_plus(uint32_t lo, uint32_t hi, uint32_t* out) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t bad = 0, first = 0xFFFFFFFFu;
+  for (uint64_t i = lo + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hi; i += stride) {
+    const float e = __uint_as_float((uint32_t)i);
+    const float fast = div_one_plus(e);
+    const float ieee = e / (1.0f + e);
+    if (__float_as_uint(fast) != __float_as_uint(ieee)) {
+      ++bad;
+      first = min(first, (uint32_t)i);
+    }
+  }
+  if (bad) {
+    atomicAdd(&out[0], bad);
+    atomicMin(&out[1], first);
+  }
+}
+
+// x = -(pattern as f32) for patterns of non-negative finite floats: every
+// x <= 0. Inputs with floor(max(x, -88) log2 e) = -127 are counted in out[2].
+__global__ void k_probe_exp_fast(uint32_t lo, uint32_t hi, uint32_t* out) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t bad = 0, first = 0xFFFFFFFFu, outside = 0;
+  for (uint64_t i = lo + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hi; i += stride) {
+    const float x = -__uint_as_float((uint32_t)i);
+    const float y = fmaxf(x, -88.0f) * 1.44269504088896340736f;
+    const bool edge = floorf(y) < -126.0f;
+    if (__float_as_uint(exp_approx_fast(x)) != __float_as_uint(exp_approx(x))) {
+      if (edge) {
+        ++outside;
+      } else {
+        ++bad;
+        first = min(first, (uint32_t)i);
+      }
+    }
+  }
+  if (bad) {
+    atomicAdd(&out[0], bad);
+    atomicMin(&out[1], first);
+  }
+  if (outside) atomicAdd(&out[2], outside);
+}
+
 }  // namespace
+
+void probe_fast_math(pfhip_backend* b, int which, uint32_t lo, uint32_t hi, uint32_t* out) {
+  PF_CHECK(lo <= hi, "probe_fast_math: empty range");
+  ProfScope ps(b, "probe_fast_math");
+  if (which == 0)
+    hipLaunchKernelGGL(k_probe_div_one_plus, dim3(8192), dim3(256), 0, b->stream, lo, hi, out);
+  else
+    hipLaunchKernelGGL(k_probe_exp_fast, dim3(8192), dim3(256), 0, b->stream, lo, hi, out);
+  PF_HIP(hipGetLastError());
+}
 
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D) {

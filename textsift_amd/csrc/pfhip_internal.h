@@ -45,6 +45,7 @@ struct ProfPending {
 
 struct pfhip_backend {
   int device = 0;
+  int num_cus = 256;  // compute units of the device
   hipStream_t stream = nullptr;
   std::string device_name;
   bool encoder_open = false;
@@ -201,6 +202,11 @@ void qmoe_gate_up_ref(pfhip_backend* b, const float* x, const int32_t* ridx, con
 void qmoe_down_scatter_ref(pfhip_backend* b, const float* glu, const int32_t* ridx, const float* rw,
                            const uint8_t* w, const uint16_t* ws, const uint8_t* wz, const uint16_t* bias, float* acc,
                            int T, int K, int N, int D);
+
+// Exhaustive checks of the fast math helpers (tests only): which = 0 checks
+// div_one_plus against IEEE division, 1 checks exp_approx_fast against
+// exp_approx. out: [mismatches, first mismatching bit pattern, outside-domain].
+void probe_fast_math(pfhip_backend* b, int which, uint32_t lo, uint32_t hi, uint32_t* out);
 
 // Layout probe for the MFMA operand assumption (tests only).
 void probe_mfma_f16(pfhip_backend* b, const uint16_t* a, const uint16_t* bm, float* d);

@@ -291,6 +291,11 @@ static std::vector<KernelEntry>& registry() {
   r.push_back({"matmul_int4_fp16_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  run_matmul(b, bs, p, false, true, "matmul_int4_fp16_f32");
                }});
+  // probe_fast_math: push {which, lo, hi}; binding [out u32 x3]
+  r.push_back({"probe_fast_math", 1, 12, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 need(bs, 0, 12, "probe_fast_math");
+                 probe_fast_math(b, (int)pu(p, 0), pu(p, 1), pu(p, 2), bp<uint32_t>(bs, 0));
+               }});
   // matmul_int4_w4: the scale-folded GEMM of the fp16 forward path (gemm_w4).
   // push {T, N, K, out_f32, tile_t, wf}; bindings [x fp16, w, scales, zp, bias, out]
   r.push_back({"matmul_int4_w4", 6, 24, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -478,6 +483,7 @@ pfhip_backend* pfhip_create_backend(int device, char* err, size_t cap) {
     b = new pfhip_backend();
     b->device = device;
     b->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    b->num_cus = prop.multiProcessorCount;
     PF_HIP(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
     return b;
   } catch (const std::exception& ex) {
