@@ -8,9 +8,21 @@ ids are uniform over the 200064-row vocabulary.
 
 Prints one JSON line with the throughput, the roofline of the dominant kernel
 (its algorithmic FLOPs per launch over its average launch time, measured with
-HIP events on the backend's stream during the timed steps) and the CPU
-baseline (the oracle's C restatement of the WASM path, multi-threaded with the
-reference's worker partitioning, on a bounded sample).
+HIP events on the backend's stream during the timed steps; the events bracket
+that kernel only, so the timed region carries no per-launch instrumentation
+of the others) and the CPU baseline (the oracle's C restatement of the WASM
+path, multi-threaded with the reference's worker partitioning, on a bounded
+sample). The per-kernel table comes from a separate profiled pass after the
+warmup. roofline.traffic (HBM bytes per launch) is read from the committed
+profiles/<kernel>_traffic.md, produced by the two rocprofv3 --pmc passes that
+--traffic-report turns into that summary.
+
+Modes beside the default:
+  --copy-calibration-mb N   also run one plain device copy of N MiB (for the
+                            PMC passes: the counters' bytes-per-byte factor)
+  --traffic-report FETCH_CSV WRITE_CSV --copy-mb N
+                            turn two rocprofv3 --pmc counter_collection.csv
+                            files into the traffic summary (markdown)
 """
 import argparse
 import json
@@ -26,6 +38,104 @@ if ROOT not in sys.path:
 
 MFMA_FP16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 HBM_PEAK_GBS = 8000.0
+
+# rocprofv3 kernel symbols -> the launch names the backend profiles under
+KERNEL_LABELS = [
+    ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true>")),
+    ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true>")),
+    ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false>")),
+    ("gemm_o", ("k_gemm_w4<5, 64", "(pf::Epi)0, false>")),
+    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)1, false>")),
+    ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false>")),
+    ("banded_attention", ("k_banded_attention",)),
+    ("moe_combine_norm", ("k_moe_combine",)),
+    ("add_rmsnorm_f16", ("k_add_rms_norm",)),
+    ("router_topk", ("k_router_topk",)),
+    ("moe_count", ("k_moe_count",)),
+    ("moe_scan", ("k_moe_scan",)),
+    ("moe_scatter", ("k_moe_scatter",)),
+    ("embed_lookup_int4", ("k_embed",)),
+    ("rms_norm", ("k_rms_norm",)),
+    ("copy", ("k_copy16",)),
+]
+
+
+def label_of(symbol):
+    for label, parts in KERNEL_LABELS:
+        if all(p in symbol for p in parts):
+            return label
+    return None
+
+
+def read_counters(path, counter):
+    """{dispatch id: (kernel symbol, value)} from a rocprofv3 counter_collection.csv."""
+    import csv
+    out = {}
+    with open(path, newline="") as f:
+        rows = csv.reader(f)
+        header = next(rows)
+        ci, vi = header.index("Counter_Name"), header.index("Counter_Value")
+        ki, di = header.index("Kernel_Name"), header.index("Dispatch_Id")
+        for r in rows:
+            # kernel symbols may contain commas: fields after Kernel_Name are counted from the end
+            name = ",".join(r[ki:len(r) - (len(header) - ki - 1)])
+            tail = r[len(r) - (len(header) - ki - 1):]
+            cn, cv = tail[ci - ki - 1], float(tail[vi - ki - 1])
+            if cn != counter:
+                continue
+            d = int(r[di])
+            prev = out.get(d, (name, 0.0))
+            out[d] = (name, prev[1] + cv)
+    return out
+
+
+def traffic_report(fetch_csv, write_csv, copy_mb):
+    """Markdown summary: per kernel, FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch) scaled by what the counters read for a plain copy of copy_mb MiB."""
+    fetch = read_counters(fetch_csv, "FETCH_SIZE")
+    write = read_counters(write_csv, "WRITE_SIZE")
+    expect_kib = copy_mb * 1024.0
+    def per_label(d):
+        acc = {}
+        for name, v in d.values():
+            lab = label_of(name)
+            if lab:
+                acc.setdefault(lab, []).append(v)
+        return acc
+    fl, wl = per_label(fetch), per_label(write)
+    copy_f = max(fl.get("copy", [0.0]))
+    copy_w = max(wl.get("copy", [0.0]))
+    kf = copy_f / expect_kib if copy_f else None
+    kw = copy_w / expect_kib if copy_w else None
+    lines = ["| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/launch |",
+             "|---|---|---|---|---|"]
+    summary = {}
+    for lab, _ in KERNEL_LABELS:
+        if lab == "copy" or lab not in fl or lab not in wl:
+            continue
+        f = sum(fl[lab]) / len(fl[lab])
+        w = sum(wl[lab]) / len(wl[lab])
+        hbm = (f / kf + w / kw) * 1024.0 if kf and kw else None
+        summary[lab] = hbm
+        lines.append(f"| {lab} | {len(fl[lab])} | {f:.1f} | {w:.1f} | {hbm:.4g} |" if hbm else
+                     f"| {lab} | {len(fl[lab])} | {f:.1f} | {w:.1f} | - |")
+    head = [f"calibration copy of {copy_mb} MiB: FETCH_SIZE {copy_f:.1f} KiB (factor {kf:.4f}), "
+            f"WRITE_SIZE {copy_w:.1f} KiB (factor {kw:.4f}); HBM bytes/launch = (FETCH/f_fetch + WRITE/f_write) * 1024",
+            ""] if kf and kw else ["no calibration copy found", ""]
+    tail = [""] + [f"hbm_bytes_per_launch {lab}: {int(v)}" for lab, v in summary.items() if v]
+    return "\n".join(head + lines + tail)
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed traffic summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith(f"hbm_bytes_per_launch {kernel}:"):
+                return int(line.split(":")[1])
+    return None
 
 
 def gemm_flops(cfg, M):
@@ -72,11 +182,19 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--profile-steps", type=int, default=2, help="steps of the all-kernel profiled pass")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0)
+    ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--copy-mb", type=int, default=1024)
     args = ap.parse_args()
+
+    if args.traffic_report:
+        print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb))
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the forward shards as independent sequences per GPU, see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the forward shards as independent sequences, one process per GPU)", file=sys.stderr)
         sys.exit(2)
 
     from textsift_amd import _native, synth
@@ -101,15 +219,33 @@ def main():
     for _ in range(args.warmup):
         model.forward_device(ids_buf, None, B, T, logits_buf)
 
-    if not args.no_profile:
+    if args.copy_calibration_mb:
+        n = args.copy_calibration_mb << 20
+        src, dst = be.buffer(nbytes=n), be.buffer(nbytes=n)
+        be.dispatch("copy16", [src, dst], np.array([n], np.uint32))
+        src.release()
+        dst.release()
+
+    # per-kernel table: a separate profiled pass with every launch bracketed
+    prof, dom = {}, None
+    if not args.no_profile and args.profile_steps > 0:
         be.profile(True)
+        be.profile_select(None)
         be.profile_reset()
+        for _ in range(args.profile_steps):
+            model.forward_device(ids_buf, None, B, T, logits_buf)
+        prof = be.profile_report()
+        dom = max(prof.items(), key=lambda kv: kv[1][1])[0]
+        # the timed region brackets the dominant kernel only
+        be.profile_reset()
+        be.profile_select(dom)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         model.forward_device(ids_buf, None, B, T, logits_buf)
     t1 = time.perf_counter()
-    prof = be.profile_report() if not args.no_profile else {}
+    dom_prof = be.profile_report().get(dom) if dom else None
     be.profile(False)
+    be.profile_select(None)
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
     tok_s = M / (ms_per_step / 1000.0)
 
@@ -124,15 +260,16 @@ def main():
     kernels = {}
     if prof:
         for name, (n, ms) in prof.items():
-            kernels[name] = {"launches": n, "avg_us": round(1000.0 * ms / n, 3), "total_ms_per_step": round(ms / args.steps, 4)}
-        dom = max(prof.items(), key=lambda kv: kv[1][1])[0]
-        n, ms = prof[dom]
+            kernels[name] = {"launches": n, "avg_us": round(1000.0 * ms / n, 3),
+                             "total_ms_per_step": round(ms / args.profile_steps, 4)}
+    if dom_prof and dom in flops:
+        n, ms = dom_prof
         avg_s = ms / n / 1000.0
-        if dom in flops:
-            achieved = flops[dom] / avg_s / 1e12
-            roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_FP16_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": None,
-                    "flops_per_launch": flops[dom], "avg_launch_us": round(avg_s * 1e6, 2)}
+        achieved = flops[dom] / avg_s / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_FP16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": read_traffic(dom),
+                "flops_per_launch": flops[dom], "avg_launch_us": round(avg_s * 1e6, 2),
+                "launches_timed": n}
     total_flops = sum(flops[k] * cfg.num_layers for k in
                       ("gemm_qkv_rope", "gemm_o", "gemm_router", "gemm_moe_gate_up", "gemm_moe_down",
                        "banded_attention")) + flops["gemm_classifier"]

@@ -164,6 +164,9 @@ int pfhip_rope_tables(const pfhip_model_config* cfg, uint32_t T, uint16_t* cos_t
  * name. report() writes "name launches total_ms" lines.
  * --------------------------------------------------------------------- */
 int pfhip_profile_enable(pfhip_backend* b, int on);
+/* Restricts recording to launches named `name` (NULL or "" = every launch),
+ * so a timed region can bracket one kernel without timing all of them. */
+int pfhip_profile_select(pfhip_backend* b, const char* name);
 int pfhip_profile_reset(pfhip_backend* b);
 int pfhip_profile_report(pfhip_backend* b, char* out, size_t cap);
 

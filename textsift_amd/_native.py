@@ -78,6 +78,7 @@ EXPORTS = [
     ("pfhip_model_enable_taps", C.c_int, [C.c_void_p, C.c_int]),
     ("pfhip_rope_tables", C.c_int, [C.POINTER(ModelConfigC), C.c_uint32, C.c_void_p, C.c_void_p]),
     ("pfhip_profile_enable", C.c_int, [C.c_void_p, C.c_int]),
+    ("pfhip_profile_select", C.c_int, [C.c_void_p, C.c_char_p]),
     ("pfhip_profile_reset", C.c_int, [C.c_void_p]),
     ("pfhip_profile_report", C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
 ]
@@ -178,6 +179,9 @@ class Backend:
 
     def profile(self, on: bool = True):
         lib().pfhip_profile_enable(self.handle, int(on))
+
+    def profile_select(self, name: str | None):
+        lib().pfhip_profile_select(self.handle, None if name is None else name.encode())
 
     def profile_reset(self):
         lib().pfhip_profile_reset(self.handle)

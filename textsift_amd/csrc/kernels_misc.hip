@@ -724,7 +724,23 @@ __global__ void k_probe_exp_fast(uint32_t lo, uint32_t hi, uint32_t* out) {
   if (outside) atomicAdd(&out[2], outside);
 }
 
+// Plain 16-byte copy (the known-size workload the HBM counters are scaled by).
+__global__ void k_copy16(const u4_t* __restrict__ src, u4_t* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 }  // namespace
+
+void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes) {
+  PF_CHECK(bytes % 16 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0,
+           "copy16: 16-byte aligned sizes and pointers");
+  if (!bytes) return;
+  ProfScope ps(b, "copy16");
+  hipLaunchKernelGGL(k_copy16, dim3(4096), dim3(256), 0, b->stream, static_cast<const u4_t*>(src),
+                     static_cast<u4_t*>(dst), bytes / 16);
+  PF_HIP(hipGetLastError());
+}
 
 void probe_fast_math(pfhip_backend* b, int which, uint32_t lo, uint32_t hi, uint32_t* out) {
   PF_CHECK(lo <= hi, "probe_fast_math: empty range");

@@ -51,6 +51,7 @@ struct pfhip_backend {
   bool encoder_open = false;
   // profiling
   bool profiling = false;
+  std::string profile_only;  // record only launches of this name ("" = all)
   std::vector<pf::ProfPending> pending;
   std::vector<hipEvent_t> event_pool;
   std::map<std::string, std::pair<long, double>> prof;  // name -> (launches, total ms)
@@ -202,6 +203,9 @@ void qmoe_gate_up_ref(pfhip_backend* b, const float* x, const int32_t* ridx, con
 void qmoe_down_scatter_ref(pfhip_backend* b, const float* glu, const int32_t* ridx, const float* rw,
                            const uint8_t* w, const uint16_t* ws, const uint8_t* wz, const uint16_t* bias, float* acc,
                            int T, int K, int N, int D);
+
+// Plain device copy of `bytes` (multiple of 16, 16-byte aligned).
+void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes);
 
 // Exhaustive checks of the fast math helpers (tests only): which = 0 checks
 // div_one_plus against IEEE division, 1 checks exp_approx_fast against

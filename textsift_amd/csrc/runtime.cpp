@@ -22,7 +22,7 @@ void set_err(char* err, size_t cap, const std::string& msg) {
 }
 
 ProfScope::ProfScope(pfhip_backend* b_, const char* n) : b(b_), name(n) {
-  if (b && b->profiling) {
+  if (b && b->profiling && (b->profile_only.empty() || b->profile_only == n)) {
     if (b->event_pool.size() >= 2) {
       start = b->event_pool.back();
       b->event_pool.pop_back();
@@ -290,6 +290,13 @@ static std::vector<KernelEntry>& registry() {
                }});
   r.push_back({"matmul_int4_fp16_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  run_matmul(b, bs, p, false, true, "matmul_int4_fp16_f32");
+               }});
+  // copy16: bindings [src, dst], push {bytes} (a plain copy of known size)
+  r.push_back({"copy16", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const size_t n = pu(p, 0);
+                 need(bs, 0, n, "copy16");
+                 need(bs, 1, n, "copy16");
+                 copy16(b, bs[0]->ptr, bs[1]->ptr, n);
                }});
   // probe_fast_math: push {which, lo, hi}; binding [out u32 x3]
   r.push_back({"probe_fast_math", 1, 12, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -665,6 +672,12 @@ int pfhip_profile_enable(pfhip_backend* b, int on) {
     return -1;
   }
   b->profiling = on != 0;
+  return 0;
+}
+
+int pfhip_profile_select(pfhip_backend* b, const char* name) {
+  if (!b) return -1;
+  b->profile_only = name ? name : "";
   return 0;
 }
 
