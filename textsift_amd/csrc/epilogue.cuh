@@ -91,6 +91,18 @@ __device__ __forceinline__ u2_t rope_f16x4(const float v[4], f2_t cs, f2_t sn) {
   return pack4(hb);
 }
 
+// Stores 4 packed fp16 values at out[orow][n..n+3] (columns past N dropped).
+__device__ __forceinline__ void store_f16x4(const GemmArgs& p, size_t orow, int n, u2_t hv) {
+  uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
+  if (n + 3 < p.N) {
+    *reinterpret_cast<u2_t*>(o) = hv;
+  } else {
+    const uint32_t w2[2] = {hv.x, hv.y};
+    for (int r = 0; r < 4; ++r)
+      if (n + r < p.N) o[r] = (uint16_t)(w2[r >> 1] >> (16 * (r & 1)));
+  }
+}
+
 // Writes v (bias already added) for output row orow, columns n..n+3.
 //   F32 / F16: out[orow][n..n+3]
 //   ROPE_F16: fp16 with RoPE on columns below rope_cols (head_dim 64);
@@ -120,14 +132,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
     } else {
       hv = to_f16x4(v);
     }
-    uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
-    if (n + 3 < p.N) {
-      *reinterpret_cast<u2_t*>(o) = hv;
-    } else {
-      const uint32_t w2[2] = {hv.x, hv.y};
-      for (int r = 0; r < 4; ++r)
-        if (n + r < p.N) o[r] = (uint16_t)(w2[r >> 1] >> (16 * (r & 1)));
-    }
+    store_f16x4(p, orow, n, hv);
   } else {
     const float g0 = swiglu_clamp_fast(v[0], v[1]);
     const float g1 = swiglu_clamp_fast(v[2], v[3]);

@@ -168,16 +168,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  load_x(0, 0);
-  load_w(0, wraw, sz);
-  for (int c = 0; c < C; ++c) {
-    const int buf = c & 1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (c + 1 < C) {
-      load_x(c + 1, buf ^ 1);
-      load_w(c + 1, wnext, sznext);
-    }
+  // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
+  auto compute = [&](int buf) {
     h2_t off[WF], sc[WF];
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
@@ -205,24 +197,89 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
         }
       }
     }
-    if (c + 1 < C) {
+  };
+
+  load_x(0, 0);
+  load_w(0, wraw, sz);
+  for (int c = 0; c + 1 < C; ++c) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    load_x(c + 1, (c & 1) ^ 1);
+    load_w(c + 1, wnext, sznext);
+    compute(c & 1);
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      wraw[f] = wnext[f];
+      sz[f] = sznext[f];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // ---- epilogue operands, loaded before the last chunk's MFMAs so that their
+  // latency overlaps them: the bias of the lane's 4 columns of every fragment
+  // and, for RoPE, the table entries of the first fragment's rows. Every load
+  // is unconditional (indices clamped); columns and rows past the edges are
+  // never stored.
+  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
+  int ncol[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * WF + f) * 16 + 4 * lg;
+  u2_t braw[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) braw[f] = u2_t{0u, 0u};
+  if (BIAS) {
+    if ((p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(BIAS) & 7) == 0) {
+#pragma unroll
+      for (int f = 0; f < WF; ++f) braw[f] = *reinterpret_cast<const u2_t*>(BIAS + min(ncol[f], p.N - 4));
+    } else {
 #pragma unroll
       for (int f = 0; f < WF; ++f) {
-        wraw[f] = wnext[f];
-        sz[f] = sznext[f];
+        uint32_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = BIAS[min(ncol[f] + r, p.N - 1)];
+        braw[f] = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
     }
   }
+  // RoPE: the table rows (32 cos + 32 sin f32 = 256 bytes, the size of an
+  // activation row) of the tile's BT positions are copied into the LDS buffer
+  // the last chunk does not use, swizzled like the activations so that the
+  // epilogue's reads are conflict-free. Row r of the tile is at position
+  // (row0 + r) mod seq_len.
+  if constexpr (EPI == Epi::ROPE_F16) {
+    const int p0 = (int)((uint32_t)row0 % (uint32_t)p.seq_len);
+    _Float16* tb = xs_lds + (C & 1) * XS * PLANE;
+#pragma unroll
+    for (int m = 0; m < XI; ++m) {
+      const int r = (m * NW + wave) * 4 + lg;
+      int q = p0 + r;
+      if (p.seq_len >= BT) q = q >= p.seq_len ? q - p.seq_len : q;
+      else q %= p.seq_len;
+      const int u = l16 ^ (r & 15);  // this lane's 16-byte unit lands at position l16 of row r
+      const float* src = (u < 8 ? p.rope_cos + u * 4 : p.rope_sin + (u - 8) * 4) + (size_t)q * 32;
+      copy16_to_lds(src, (lds_ptr_t)(tb + (m * NW + wave) * 512));
+    }
+  }
+
+  compute((C - 1) & 1);
+  if constexpr (EPI == Epi::ROPE_F16) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
 
   // ---- epilogue: lane holds out[token = 16 tj + l16][n = n0 + (wave WF + f) 16 + 4 lg + r]
-  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
-    const int n = n0 + (wave * WF + f) * 16 + 4 * lg;
+    const int n = ncol[f];
     if (n >= p.N) continue;
+    const uint32_t bw[2] = {braw[f].x, braw[f].y};
     float bv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) bv[r] = (BIAS && n + r < p.N) ? wasm_h2f(BIAS[n + r]) : 0.0f;
+    for (int r = 0; r < 4; ++r) bv[r] = n + r < p.N ? wasm_h2f((uint16_t)(bw[r >> 1] >> (16 * (r & 1)))) : 0.0f;
+    // a fragment of 16 columns lies wholly below or above rope_cols (a multiple of 64)
+    const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
+    const int pidx = (n & 63) >> 1;  // this lane's first (cos, sin) pair of the head
 #pragma unroll
     for (int tj = 0; tj < TJ; ++tj) {
       const int lt = 16 * tj + l16;
@@ -231,9 +288,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = acc[f][tj][r] + bv[r];
-      int pos = 0;
-      if constexpr (EPI == Epi::ROPE_F16) pos = (int)((uint32_t)orow % (uint32_t)p.seq_len);  // rows < 2^31
-      store_out<EPI>(p, orow, n, v, pos);
+      if constexpr (EPI == Epi::ROPE_F16) {
+        u2_t hv;
+        if (rope) {
+          const char* trow = reinterpret_cast<const char*>(xs_lds + (C & 1) * XS * PLANE) + lt * 256;
+          const int ucs = (pidx >> 2) ^ l16, usn = ((pidx >> 2) + 8) ^ l16;  // row lt: (lt & 15) == l16
+          const f2_t cs = *reinterpret_cast<const f2_t*>(trow + ucs * 16 + (pidx & 3) * 4);
+          const f2_t sn = *reinterpret_cast<const f2_t*>(trow + usn * 16 + (pidx & 3) * 4);
+          hv = rope_f16x4(v, cs, sn);
+        } else {
+          hv = to_f16x4(v);
+        }
+        store_f16x4(p, orow, n, hv);
+      } else {
+        store_out<EPI>(p, orow, n, v);
+      }
     }
   }
 }
