@@ -170,6 +170,25 @@ int pfhip_profile_select(pfhip_backend* b, const char* name);
 int pfhip_profile_reset(pfhip_backend* b);
 int pfhip_profile_report(pfhip_backend* b, char* out, size_t cap);
 
+/* ------------------------------------------------------------------------
+ * Host-side span decoding of the forward's logits.
+ *
+ * ViterbiDecoder.decode (packages/textsift/src/browser/inference/viterbi.ts:
+ * 85-146, tables :159-219): the most likely BIOES tag sequence of each of
+ * `batch` sequences. logits: f32 [batch][seq_stride][num_classes] (row-major,
+ * as Logits.data); seq_lens: tokens to decode per sequence (<= seq_stride;
+ * NULL = all seq_stride), like decode()'s sequenceLength argument; biases: the
+ * six calibration biases in model/calibration.ts:29-36 order
+ * (backgroundStay, backgroundToStart, insideToContinue, insideToEnd,
+ * endToBackground, endToStart); tags: u8 [batch][seq_stride] (entries past a
+ * sequence's length are left untouched). num_classes must be 33, as the
+ * reference requires. Sequences are decoded on up to n_threads host threads
+ * (0 = one per host core). Runs on the host only; no device is touched.
+ * --------------------------------------------------------------------- */
+int pfhip_viterbi_decode(const float* logits, uint32_t batch, uint32_t seq_stride, const uint32_t* seq_lens,
+                         uint32_t num_classes, const float* biases, uint8_t* tags, uint32_t n_threads, char* err,
+                         size_t err_cap);
+
 /* Library version string. */
 const char* pfhip_version(void);
 

@@ -55,3 +55,80 @@ def dequant_rows(int4, scales, zp, n_rows, k):
 def fp16_ieee(x):
     """float -> fp16 bits with IEEE RNE, subnormals kept (for expected values)."""
     return np.asarray(x, np.float64).astype(np.float16).view(np.uint16)
+
+
+class WordTokenizer:
+    """Test tokenizer with the reference Tokenizer's encode() contract
+    (browser/model/tokenizer.ts:240-305): word pieces carrying their leading
+    space, as ByteLevel BPE does; token_to_char_offset has n + 1 entries (the
+    last is the end of the last token). Ids are a stable hash of the piece
+    modulo `vocab`."""
+
+    def __init__(self, vocab=200064):
+        import re
+        self._re = re.compile(r"\s?\w+|\s?[^\w\s]+|\s+")
+        self._vocab = vocab
+
+    def encode(self, text):
+        import types
+        import zlib
+        ms = list(self._re.finditer(text))
+        return types.SimpleNamespace(
+            token_ids=np.array([zlib.crc32(m.group().encode()) % self._vocab for m in ms], np.int32),
+            attention_mask=np.ones(len(ms), np.uint8),
+            token_to_char_offset=[m.start() for m in ms] + [ms[-1].end() if ms else 0],
+            words=[m.group() for m in ms])
+
+    def labels(self):
+        from textsift_amd.spans import ALL_SPAN_LABELS
+        return ALL_SPAN_LABELS
+
+
+def random_words(n, seed):
+    rng = np.random.default_rng(seed)
+    vocab = ["alpha", "beta", "Gamma", "delta", "Eps", "zeta", "eta", ",", "theta", "Iota", "kappa", "Lambda",
+             "mu@nu.io", "(617)", "555-0199", "42"]
+    return " ".join(vocab[i] for i in rng.integers(0, len(vocab), n))
+
+
+def span_parity(got, ref, chunk, labels=None):
+    """Spans of two logit grids [T, 33] (Viterbi with the zero calibration,
+    then BIOES -> spans over `chunk`), compared.
+
+    Returns (identical, report). When the tag paths differ, `report` holds
+    the evidence that the difference is a near-tie the logit error explains:
+    with every transition score 0 for legal moves, a path's score is the sum
+    of its logits, so for the GPU path p (optimal for `got`) and the oracle's
+    q (optimal for `ref`), S_ref(q) - S_ref(p) <= sum over tokens where the
+    paths differ of |d[t, p_t] - d[t, q_t]|, d = got - ref. A decoder or
+    logit bug that is not a near-tie breaks that bound."""
+    from textsift_amd.spans import ALL_SPAN_LABELS, ViterbiDecoder, bioes_to_spans, zero_calibration
+    labels = labels or ALL_SPAN_LABELS
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    dec = ViterbiDecoder(zero_calibration())
+    p, q = dec.decode(got).astype(np.int64), dec.decode(ref).astype(np.int64)
+    key = lambda s: (s.label, s.start, s.end)
+    sg = [key(s) for s in bioes_to_spans(p, chunk, labels)]
+    sr = [key(s) for s in bioes_to_spans(q, chunk, labels)]
+    diff = np.nonzero(p != q)[0]
+    t = np.arange(p.size)
+    g64, r64 = got.astype(np.float64), ref.astype(np.float64)
+    gap = float(r64[t, q].sum() - r64[t, p].sum())
+    d = g64 - r64
+    bound = float(np.abs(d[diff, p[diff]] - d[diff, q[diff]]).sum())
+    # spans away from the differing tokens must agree exactly
+    offs = chunk.token_to_char_offset
+    bad_chars = [(chunk.char_offset + offs[i], chunk.char_offset + offs[i + 1]) for i in diff]
+    touches = lambda s: any(s[1] < e and b < s[2] for b, e in bad_chars)
+    rest_equal = [s for s in sg if not touches(s)] == [s for s in sr if not touches(s)]
+    report = {"n_spans": len(sr), "diff_tokens": int(diff.size), "gap": gap, "bound": bound,
+              "rest_equal": rest_equal}
+    return sg == sr, report
+
+
+def near_tie_only(report, T, max_frac=0.01):
+    """True if a span difference is a near-tie of the kind span_parity
+    describes, on at most max_frac of the tokens."""
+    return (report["rest_equal"] and report["diff_tokens"] <= max_frac * T
+            and report["gap"] <= report["bound"] * (1 + 1e-6) + 1e-3)

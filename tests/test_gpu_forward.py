@@ -10,10 +10,11 @@ import numpy as np
 import pytest
 
 import oracle
-from parity_util import f16, rel_err_norm
+from parity_util import f16, near_tie_only, rel_err_norm, span_parity
 from textsift_amd import _native, synth
 from textsift_amd.backend import HipBackend
 from textsift_amd.config import PF_CONFIG
+from textsift_amd.spans import ALL_SPAN_LABELS, Chunk, ViterbiDecoder, bioes_to_spans, zero_calibration
 
 pytestmark = pytest.mark.gpu
 
@@ -112,6 +113,11 @@ def test_per_layer_taps_vs_oracle_block(small):
     m.enable_taps(False)
 
 
+def _synthetic_chunk(T):
+    """T two-character tokens without whitespace."""
+    return Chunk(np.zeros(T, np.int32), np.ones(T, np.uint8), list(range(0, 2 * T + 1, 2)), "ab" * T, 0, (0, T))
+
+
 @pytest.fixture(scope="module")
 def full_ref():
     """Oracle logits of the full-size model for one T=2048 sequence."""
@@ -134,8 +140,43 @@ def test_full_model_forward_vs_oracle(full_ref, precision):
         got = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
         err = rel_err_norm(got, ref)
         agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
-        print(f"full model T={T} precision={precision}: rel-err {err:.3e}, argmax agreement {agree:.5f}")
+        same, rep = span_parity(got, ref, _synthetic_chunk(T))
+        print(f"full model T={T} precision={precision}: rel-err {err:.3e}, argmax agreement {agree:.5f}, "
+              f"spans identical {same} {rep}")
         assert err < 2e-3
         assert agree >= 0.999
+        assert same or near_tie_only(rep, T)
     finally:
         be.dispose()
+
+
+def test_detect_spans_vs_oracle(small):
+    """detect() through the HIP backend (full-length chunks in one batched
+    forward) gives the spans of the oracle's logits pushed through the same
+    chunking, Viterbi and merge (the north star's "identical final spans")."""
+    from parity_util import WordTokenizer, random_words
+    from textsift_amd.spans import chunk_input, detect, merge_chunk_results
+
+    w, be = small
+    tok = WordTokenizer(V)
+    text = random_words(700, 17)
+    dec = ViterbiDecoder(zero_calibration())
+    got = detect(text, be, tok, dec, max_chunk_tokens=512)
+    chunks = chunk_input(text, tok, 512)
+    assert len(chunks) >= 3
+    per = []
+    for c in chunks:
+        ref = f16(oracle.model_forward(PF_CONFIG, w, c.token_ids, num_layers=L)).astype(np.float32)
+        per.append(bioes_to_spans(dec.decode(ref), c, ALL_SPAN_LABELS))
+    want = merge_chunk_results(per, chunks)
+    key = lambda s: (s.label, s.start, s.end)
+    same = [key(s) for s in got] == [key(s) for s in want]
+    print(f"detect: {len(chunks)} chunks, {len(want)} spans, identical {same}")
+    if not same:
+        # the spans may differ only where a chunk's Viterbi paths differ by a near-tie
+        for c in chunks:
+            g = be.forward(c.token_ids, c.attention_mask).as_matrix()
+            r = f16(oracle.model_forward(PF_CONFIG, w, c.token_ids, num_layers=L)).astype(np.float32)
+            ok, rep = span_parity(g, r, c)
+            print(f"  chunk of {c.token_ids.size} tokens: identical {ok} {rep}")
+            assert ok or near_tie_only(rep, c.token_ids.size)

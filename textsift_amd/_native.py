@@ -81,6 +81,8 @@ EXPORTS = [
     ("pfhip_profile_select", C.c_int, [C.c_void_p, C.c_char_p]),
     ("pfhip_profile_reset", C.c_int, [C.c_void_p]),
     ("pfhip_profile_report", C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t]),
+    ("pfhip_viterbi_decode", C.c_int, [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p,
+                                       C.c_void_p, C.c_uint32, C.c_char_p, C.c_size_t]),
 ]
 
 
@@ -268,3 +270,29 @@ def rope_tables(cfg, T: int):
     if lib().pfhip_rope_tables(C.byref(c), T, _ptr(cs), _ptr(sn)) != 0:
         raise PfhipError("rope_tables failed")
     return cs, sn
+
+
+def viterbi_decode(logits: np.ndarray, biases, seq_lens=None, n_threads: int = 0) -> np.ndarray:
+    """BIOES Viterbi decode on the host (pfhip_viterbi_decode).
+    logits: f32 [T, C] or [B, T, C]; biases: the six calibration biases;
+    seq_lens: tokens to decode per sequence (default: all). Returns u8 tags
+    of logits' leading shape (entries past a sequence's length are 0)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    single = lg.ndim == 2
+    if single:
+        lg = lg[None]
+    if lg.ndim != 3:
+        raise ValueError("viterbi_decode: logits must be [T, C] or [B, T, C]")
+    B, T, Cn = lg.shape
+    bias = np.ascontiguousarray(biases, np.float32).ravel()
+    if bias.size != 6:
+        raise ValueError("viterbi_decode: expected 6 calibration biases")
+    lens = None
+    if seq_lens is not None:
+        lens = np.ascontiguousarray(np.broadcast_to(np.asarray(seq_lens, np.uint32), (B,)), np.uint32)
+    tags = np.zeros((B, T), np.uint8)
+    err = _err()
+    rc = lib().pfhip_viterbi_decode(_ptr(lg), B, T, None if lens is None else _ptr(lens), Cn, _ptr(bias),
+                                    _ptr(tags), n_threads, err, ERR_CAP)
+    _check(rc, err, "viterbi_decode")
+    return tags[0] if single else tags
