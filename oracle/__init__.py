@@ -72,6 +72,8 @@ def lib():
         _lib.pfo_scatter_add_weighted_f32.argtypes = [C.c_void_p] * 4 + [C.c_uint32] * 2
         _lib.pfo_cast_f32_to_fp16_scaled.argtypes = [C.c_void_p] * 2 + [C.c_uint32, C.c_float]
         _lib.pfo_banded_attention.argtypes = [C.c_void_p] * 6 + [C.c_uint32] * 7
+        _lib.pfo_banded_attention_wgsl.argtypes = [C.c_void_p] * 6 + [C.c_uint32] * 5
+        _lib.pfo_f2h_ieee.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         _lib.pfo_rope_apply.argtypes = [C.c_void_p] * 3 + [C.c_uint32] * 3
         _lib.pfo_embed_lookup_int4.argtypes = [C.c_void_p] * 5 + [C.c_uint32] * 3
         _lib.pfo_rope_tables.argtypes = [C.POINTER(Config), C.c_uint32, C.c_void_p, C.c_void_p]
@@ -202,6 +204,23 @@ def banded_attention(q, k, v, sinks, mask, T, Hq, Hkv, hd, window, h0=0, h1=None
     out = np.zeros((T, Hq * hd), np.uint16)
     lib().pfo_banded_attention(_p(q), _p(k), _p(v), _p(sinks), _p(mask), _p(out), T, Hq, Hkv, hd, window, h0,
                                Hq if h1 is None else h1)
+    return out
+
+
+def f2h_ieee(x):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().pfo_f2h_ieee(_p(x), _p(out), x.size)
+    return out
+
+
+def banded_attention_wgsl(q, k, v, sinks, mask, T, Hq, Hkv, hd, window):
+    """The reference's GPU-path attention (native/shaders/banded_attention.wgsl)."""
+    q, k, v = _c(q, np.uint16), _c(k, np.uint16), _c(v, np.uint16)
+    sinks = _c(sinks, np.float32)
+    mask = None if mask is None else _c(mask, np.uint8)
+    out = np.zeros((T, Hq * hd), np.uint16)
+    lib().pfo_banded_attention_wgsl(_p(q), _p(k), _p(v), _p(sinks), _p(mask), _p(out), T, Hq, Hkv, hd, window)
     return out
 
 

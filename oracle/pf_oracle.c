@@ -451,6 +451,92 @@ void pfo_banded_attention(const uint16_t* q, const uint16_t* k, const uint16_t* 
   free(acc);
 }
 
+/* The reference's GPU-path attention, native/shaders/banded_attention.wgsl
+ * (one 64-thread workgroup per (query, head)): scores by a sequential f32
+ * fma over head_dim (:59-73), masked keys score NEG_INF = -1e30 (:56,72),
+ * row max over the scores and the sink (:76-96), e = exp(s - max) with the
+ * shader's exp (libm expf here; pass 2 :100-106), the sum as 64 strided
+ * per-thread partials (the sink added to thread 0's) reduced by the shader's
+ * tree (:110-126), inv = 1 / sum, p = e * inv (:131-137), then
+ * out[d] = f16(sum_i fma(p_i, v_i[d], acc)) sequentially over the keys
+ * (:141-151). fp16 values are widened IEEE-correctly (WGSL f32()) and the
+ * output rounded RNE (WGSL f16()). */
+static inline uint16_t f2h_ieee(float f) {
+  const uint32_t x = f32_bits(f), sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);  /* NaN */
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  /* rounds to inf (>= 65520) */
+  if (ax >= 0x38800000u) {                                    /* normal fp16: RNE */
+    const uint32_t m = ax - 0x38000000u;
+    return (uint16_t)(sign | ((m + 0x0fffu + ((m >> 13) & 1u)) >> 13));
+  }
+  return (uint16_t)(sign | (uint32_t)nearbyintf(bits_f32(ax) * 16777216.0f)); /* subnormal: RNE of f * 2^24 */
+}
+
+void pfo_f2h_ieee(const float* x, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] = f2h_ieee(x[i]);
+}
+
+static inline float h2f_ieee(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ffu;
+  if (e == 0) {
+    const float v = ldexpf((float)m, -24);
+    return sign ? -v : v;
+  }
+  if (e == 31) return bits_f32(sign | 0x7f800000u | (m << 13));
+  return bits_f32(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+void pfo_banded_attention_wgsl(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* sinks,
+                               const uint8_t* mask, uint16_t* out, uint32_t T, uint32_t Hq, uint32_t Hkv,
+                               uint32_t Dh, uint32_t W) {
+  const size_t group = Hq / Hkv;
+  const size_t qs = (size_t)Hq * Dh, ks = (size_t)Hkv * Dh;
+  const float NEG = -1e30f;
+  float* scores = (float*)malloc(sizeof(float) * (2 * (size_t)W + 2));
+  for (size_t tq = 0; tq < T; tq++) {
+    for (size_t hq = 0; hq < Hq; hq++) {
+      const size_t hkv = hq / group, qb = tq * qs + hq * Dh;
+      const size_t ws = tq > W ? tq - W : 0;
+      const size_t we = tq + W + 1 < T ? tq + W + 1 : T;
+      const size_t nk = we - ws;
+      float tmp[64];
+      for (int t = 0; t < 64; t++) tmp[t] = NEG;
+      for (size_t j = 0; j < nk; j++) {
+        const size_t ak = ws + j;
+        float s = NEG;
+        if (!mask || mask[ak] != 0) {
+          float dot = 0.0f;
+          for (size_t d = 0; d < Dh; d++) dot = fmaf(h2f_ieee(q[qb + d]), h2f_ieee(k[ak * ks + hkv * Dh + d]), dot);
+          s = dot;
+        }
+        scores[j] = s;
+        if (s > tmp[j % 64]) tmp[j % 64] = s;
+      }
+      if (sinks[hq] > tmp[0]) tmp[0] = sinks[hq];
+      for (int stride = 32; stride >= 1; stride /= 2)
+        for (int t = 0; t < stride; t++) tmp[t] = fmaxf(tmp[t], tmp[t + stride]);
+      const float row_max = tmp[0];
+      for (int t = 0; t < 64; t++) tmp[t] = 0.0f;
+      for (size_t j = 0; j < nk; j++) {
+        const float e = expf(scores[j] - row_max);
+        scores[j] = e;
+        tmp[j % 64] = tmp[j % 64] + e;
+      }
+      tmp[0] = tmp[0] + expf(sinks[hq] - row_max);
+      for (int stride = 32; stride >= 1; stride /= 2)
+        for (int t = 0; t < stride; t++) tmp[t] = tmp[t] + tmp[t + stride];
+      const float inv = tmp[0] > 0.0f ? 1.0f / tmp[0] : 0.0f;
+      for (size_t j = 0; j < nk; j++) scores[j] = scores[j] * inv;
+      for (size_t d = 0; d < Dh; d++) {
+        float acc = 0.0f;
+        for (size_t j = 0; j < nk; j++) acc = fmaf(scores[j], h2f_ieee(v[(ws + j) * ks + hkv * Dh + d]), acc);
+        out[qb + d] = (uint16_t)f2h_ieee(acc);
+      }
+    }
+  }
+  free(scores);
+}
+
 /* ------------------------------------------------------------------ */
 /* RoPE — :1460-1502 ; GatherBlockQuantized — :1523-1573               */
 /* ------------------------------------------------------------------ */

@@ -60,7 +60,14 @@ void pfo_banded_attention(const uint16_t* q, const uint16_t* k, const uint16_t* 
                           const float* sinks, const uint8_t* mask /* may be NULL */,
                           uint16_t* out, uint32_t T, uint32_t Hq, uint32_t Hkv,
                           uint32_t head_dim, uint32_t window,
-                          uint32_t h_q_start, uint32_t h_q_end);             /* :1286-1432 */
+                          uint32_t h_q_start, uint32_t h_q_end);
+/* IEEE f32 -> fp16 (round to nearest even, subnormals kept): WGSL f16(). */
+void pfo_f2h_ieee(const float* x, uint16_t* out, size_t n);
+/* banded_attention.wgsl (the reference's GPU path): libm exp, the shader's
+ * reduction orders, IEEE fp16 conversions. */
+void pfo_banded_attention_wgsl(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* sinks,
+                               const uint8_t* mask, uint16_t* out, uint32_t T, uint32_t Hq, uint32_t Hkv,
+                               uint32_t Dh, uint32_t W);             /* :1286-1432 */
 void pfo_rope_apply(uint16_t* qk, const uint16_t* cos_t, const uint16_t* sin_t,
                     uint32_t T, uint32_t H, uint32_t head_dim);              /* :1460-1502 */
 void pfo_embed_lookup_int4(const uint8_t* embed_int4, const uint16_t* embed_scales,

@@ -356,6 +356,54 @@ def test_banded_attention_fixture(fixture):
     assert rel_err_max(f16(got.ravel()), f16(fx.expected(np.uint16))) < 1e-3
 
 
+def test_f2h_ieee_matches_numpy():
+    """WGSL f16(): IEEE round-to-nearest-even with subnormals, on every
+    fp16 rounding boundary neighbourhood and random f32 patterns."""
+    h = np.arange(0, 0x7C00, dtype=np.uint32)
+    mid = (f16(h).astype(np.float64) + f16(h + 1).astype(np.float64)) / 2  # halfway points (exact in f32)
+    xs = np.concatenate([mid.astype(np.float32), np.nextafter(mid.astype(np.float32), np.float32(np.inf)),
+                         np.nextafter(mid.astype(np.float32), np.float32(-np.inf)), f16(h).astype(np.float32)])
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([xs, rng.integers(0, 2**32, 1 << 20, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    xs = np.concatenate([xs, -xs])
+    xs = xs[np.isfinite(xs)]
+    with np.errstate(over="ignore"):
+        want = xs.astype(np.float16).view(np.uint16)
+    got = oracle.f2h_ieee(xs)
+    nan = np.isnan(xs)
+    assert np.array_equal(got[~nan], want[~nan])
+
+
+def test_banded_attention_wgsl_fixture(fixture):
+    """The GPU-path restatement against the reference shader's own output."""
+    fx = fixture("banded_attention")
+    T, Hq, Hkv, hd, W, use_mask = fx.uniform_u32[:6]
+    mask = fx.input("mask").astype(np.uint8)[:T] if use_mask else None
+    got = oracle.banded_attention_wgsl(fx.input("q", np.uint16), fx.input("k", np.uint16), fx.input("v", np.uint16),
+                                       fx.input("sinks", np.float32), mask, T, Hq, Hkv, hd, W).ravel()
+    want = fx.expected(np.uint16)
+    assert np.mean(fp16_ulp_diff(got, want) <= 1.0) == 1.0
+    assert np.mean(got == want) > 0.95
+    assert rel_err_norm(f16(got), f16(want)) < 1e-4
+
+
+@pytest.mark.parametrize("T,W,masked", [(300, 128, False), (150, 20, True)])
+def test_banded_attention_wgsl_closed_form(T, W, masked):
+    Hq, Hkv, hd = 14, 2, 64
+    q = synth.to_fp16_bits(synth.normal(190 + T, T * Hq * hd, 0, 0.4))
+    k = synth.to_fp16_bits(synth.normal(191 + T, T * Hkv * hd, 0, 0.4))
+    v = synth.to_fp16_bits(synth.normal(192 + T, T * Hkv * hd))
+    sinks = synth.normal(193, Hq).astype(np.float32)
+    mask = (synth.uniform(194, T) > 0.3).astype(np.uint8) if masked else None
+    got = oracle.banded_attention_wgsl(q, k, v, sinks, mask, T, Hq, Hkv, hd, W)
+    ref = attention_ref64(q, k, v, sinks.astype(np.float64), mask, T, Hq, Hkv, hd, W, exp=np.exp)
+    # within 1 fp16 ulp, except near zero where the f32 sum of ~2W terms of
+    # size ~1 leaves an absolute error of a few 1e-7
+    d = fp16_ulp_diff(got, fp16_ieee(ref))
+    assert np.all((d <= 1.0) | (np.abs(f16(got) - ref) < 2e-6))
+    assert np.mean(got == fp16_ieee(ref)) > 0.99
+
+
 def exp_poly64(x):
     """float64 evaluation of expApproxNonPositiveF32x4's formula (f32 y)."""
     y = np.maximum(np.asarray(x, np.float32), np.float32(-88.0)) * np.float32(1.44269504088896340736)

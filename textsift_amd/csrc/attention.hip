@@ -48,7 +48,12 @@ __device__ __forceinline__ int wave_max_i(int v) {
 }
 
 // NW waves x 16 queries per workgroup; NCH 32-key chunks per 16-query tile.
-template <int HD, int NCH, int NW>
+// HWX: the softmax exponentials use the hardware exp2 (v_exp_f32, about 1
+// ulp) on scores pre-multiplied by log2(e), as the reference's GPU shader
+// uses the WGSL exp (src/native/shaders/banded_attention.wgsl:100-113);
+// otherwise they follow the WASM path (polynomial expApprox for the 4-lane
+// part, libm exp for the scalar tail).
+template <int HD, int NCH, int NW, bool HWX>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   constexpr int QB = 16 * NW;                // query tokens per workgroup
   constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
@@ -112,6 +117,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int any_hi = wave_max_i(q_ok ? hi0 : 0);
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
+  constexpr float LOG2_E = 1.44269504088896340736f;
+  const float sscale = HWX ? a.scale * LOG2_E : a.scale;  // scores in the exponent's units
 
   for (int hh = 0; hh < G; ++hh) {
     const int hq = g * G + hh;
@@ -128,7 +135,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
       if (q_ok) v = *reinterpret_cast<const u4_t*>(a.q + (seq0 + tq) * a.q_stride + hq * HD + 32 * dh + 8 * lg);
       qf[dh] = __builtin_bit_cast(h8_t, v);
     }
-    const float sink = a.sinks ? a.sinks[hq] : -INFINITY;
+    const float sink = a.sinks ? (HWX ? a.sinks[hq] * LOG2_E : a.sinks[hq]) : -INFINITY;
 
     // ---- pass 1: scores for the whole band, kept in registers. Slots
     // outside the query's window hold NaN; masked keys hold -inf.
@@ -152,7 +159,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float sv = acc[kt][r] * a.scale;
+            const float sv = acc[kt][r] * sscale;
             s[c][kt][r] = sv;
             m = fmaxf(m, sv);
           }
@@ -165,7 +172,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
             const bool inwin = (off >= lo) & (off < hi);
             bool valid = inwin;
             if (masked) valid = valid && a.mask[seq0 + kw + off] != 0;
-            const float sv = valid ? acc[kt][r] * a.scale : -INFINITY;
+            const float sv = valid ? acc[kt][r] * sscale : -INFINITY;
             s[c][kt][r] = inwin ? sv : NAN;
             m = valid ? fmaxf(m, sv) : m;
           }
@@ -183,13 +190,13 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const bool plain = !masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi &&
-                         !(32 * c + 32 > tail_lo && 32 * c < any_hi);
+                         (HWX || !(32 * c + 32 > tail_lo && 32 * c < any_hi));
       if (plain) {  // wave-uniform: every slot in every window, no tail key
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float e = exp_approx_fast(s[c][kt][r] - m);
+            const float e = HWX ? __builtin_amdgcn_exp2f(s[c][kt][r] - m) : exp_approx_fast(s[c][kt][r] - m);
             s[c][kt][r] = e;
             l += e;
           }
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
             const float sv = s[c][kt][r];
             const float x = sv - m;
             const int off = 32 * c + 16 * kt + 4 * lg + r;
-            float e = off >= tail ? expf(x) : exp_approx_fast(x);
+            float e = HWX ? __builtin_amdgcn_exp2f(x) : (off >= tail ? expf(x) : exp_approx_fast(x));
             e = (sv != sv) ? 0.0f : e;
             s[c][kt][r] = e;
             l += e;
@@ -211,7 +218,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
     }
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    l += n_keys < vec_end ? exp_approx_fast(sink - m) : expf(sink - m);
+    if constexpr (HWX) l += __builtin_amdgcn_exp2f(sink - m);
+    else l += n_keys < vec_end ? exp_approx_fast(sink - m) : expf(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 
     // ---- pass 3: O^T = V^T . P^T with P normalised, as fp16 hi + lo
@@ -254,20 +262,26 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   }
 }
 
-template <int HD, int NCH, int NW>
-void launch_attn(pfhip_backend* b, const AttnArgs& a) {
+template <int HD, int NCH, int NW, bool HWX>
+void launch_attn_x(pfhip_backend* b, const AttnArgs& a) {
   constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;
   const size_t lds = (size_t)(ROWS * (HD + 8) + HD * (ROWS + 8)) * sizeof(_Float16);
   static bool attr_set = false;
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_banded_attention<HD, NCH, NW>),
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_banded_attention<HD, NCH, NW, HWX>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
   dim3 grid((a.T + 16 * NW - 1) / (16 * NW), a.Hkv, a.B);
   ProfScope ps(b, "banded_attention");
-  hipLaunchKernelGGL((k_banded_attention<HD, NCH, NW>), grid, dim3(64 * NW), lds, b->stream, a);
+  hipLaunchKernelGGL((k_banded_attention<HD, NCH, NW, HWX>), grid, dim3(64 * NW), lds, b->stream, a);
   PF_HIP(hipGetLastError());
+}
+
+template <int HD, int NCH, int NW>
+void launch_attn(pfhip_backend* b, const AttnArgs& a) {
+  if (a.hw_exp) launch_attn_x<HD, NCH, NW, true>(b, a);
+  else launch_attn_x<HD, NCH, NW, false>(b, a);
 }
 
 template <int HD>

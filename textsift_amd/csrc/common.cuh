@@ -172,6 +172,23 @@ __device__ __forceinline__ float swiglu_clamp_fast(float gate_raw, float up_raw)
   return (up + 1.0f) * (gate * sigmoid_approx_fast(gate * 1.702f));
 }
 
+// SwiGLU with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; each
+// within about 1 ulp), in the form of the reference's GPU shader
+// (src/native/shaders/swiglu_clamp.wgsl:10-25): sigma(x) = 1 / (1 + exp(-x))
+// for x >= 0, else e / (1 + e) with e = exp(x). Used by the fp16 forward,
+// which follows the GPU paths' numerics; it differs from swiglu_clamp by a
+// few f32 ulps, which changes an fp16-rounded output in about one case in a
+// thousand, by one fp16 ulp.
+__device__ __forceinline__ float swiglu_clamp_hw(float gate_raw, float up_raw) {
+  const float gate = fminf(gate_raw, 7.0f);
+  const float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
+  const float x = gate * 1.702f;
+  const float e = __builtin_amdgcn_exp2f(-fabsf(x) * 1.44269504088896340736f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  const float sig = x >= 0.0f ? r : e * r;
+  return (up + 1.0f) * (gate * sig);
+}
+
 // v_mfma_f32_16x16x32_f16 (gfx950). Operand layout (lane l, i = l / 16):
 //   a: A[m = l%16][k = 8i .. 8i+7]     (16 x 32, row-major fragment)
 //   b: B[k = 8i .. 8i+7][n = l%16]     (32 x 16)

@@ -103,6 +103,16 @@ __device__ __forceinline__ void store_f16x4(const GemmArgs& p, size_t orow, int 
   }
 }
 
+// SWIGLU_F16 of one lane's (gate, up) column pairs (n, n+1), (n+2, n+3):
+// two fp16 values packed, rounded as wasm_f2h rounds.
+__device__ __forceinline__ uint32_t swiglu_f16x2(const float v[4]) {
+  const float g0 = swiglu_clamp_hw(v[0], v[1]);
+  const float g1 = swiglu_clamp_hw(v[2], v[3]);
+  uint32_t h = (uint32_t)hw_f2h(g0) | ((uint32_t)hw_f2h(g1) << 16);
+  if (!(f16_plain(g0) & f16_plain(g1))) h = to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
+  return h;
+}
+
 // Writes v (bias already added) for output row orow, columns n..n+3.
 //   F32 / F16: out[orow][n..n+3]
 //   ROPE_F16: fp16 with RoPE on columns below rope_cols (head_dim 64);
@@ -134,11 +144,13 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
     }
     store_f16x4(p, orow, n, hv);
   } else {
-    const float g0 = swiglu_clamp_fast(v[0], v[1]);
-    const float g1 = swiglu_clamp_fast(v[2], v[3]);
+    // SWIGLU_SPLIT carries the f32 result (the WASM path's numerics);
+    // SWIGLU_F16 rounds it to fp16 (the GPU paths')
     const size_t oc = (size_t)(n >> 1);
     if constexpr (EPI == Epi::SWIGLU_SPLIT) {
       // f32 SwiGLU output (expert.ts keeps it f32) as hi/lo fp16 planes
+      const float g0 = swiglu_clamp_fast(v[0], v[1]);
+      const float g1 = swiglu_clamp_fast(v[2], v[3]);
       uint16_t a0, a1, e0, e1;
       split_hilo(g0, a0, e0);
       split_hilo(g1, a1, e1);
@@ -146,9 +158,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& p, size_t orow, int n,
           (uint32_t)a0 | ((uint32_t)a1 << 16);
       *reinterpret_cast<uint32_t*>(p.out_lo + orow * p.ldo + oc) = (uint32_t)e0 | ((uint32_t)e1 << 16);
     } else {
-      uint32_t h = (uint32_t)hw_f2h(g0) | ((uint32_t)hw_f2h(g1) << 16);
-      if (!(f16_plain(g0) & f16_plain(g1))) h = to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
-      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) = h;
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + oc) = swiglu_f16x2(v);
     }
   }
 }

@@ -341,6 +341,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.sinks = L.sinks; a.mask = mask;
       a.out = s.att; a.out_stride = Hq * hd;
       a.B = B; a.T = T; a.Hq = Hq; a.Hkv = Hkv; a.head_dim = hd; a.window = (int)c.window; a.scale = 1.0f;
+      a.hw_exp = f16;
       banded_attention(b, a);
     }
     record_tap(m, "att." + tag, s.att, (size_t)M * Hq * hd * 2);

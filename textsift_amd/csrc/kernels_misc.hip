@@ -742,13 +742,38 @@ void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes) {
   PF_HIP(hipGetLastError());
 }
 
+// Hardware exp2 (v_exp_f32) on x = -(pattern as f32) against exp2 evaluated
+// in double and rounded to f32: out[0] = largest difference in f32 ulps,
+// out[1] = inputs more than 1 ulp off, out[2] = inputs more than 4 ulps off.
+// Inputs whose exact result is below the smallest normal f32 are skipped.
+__global__ void k_probe_exp2_hw(uint32_t lo, uint32_t hi, uint32_t* out) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t worst = 0, over1 = 0, over4 = 0;
+  for (uint64_t i = lo + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hi; i += stride) {
+    const float x = -__uint_as_float((uint32_t)i);
+    if (!(x >= -126.0f)) continue;
+    const float hw = __builtin_amdgcn_exp2f(x);
+    const float ref = (float)exp2((double)x);
+    const int32_t d = (int32_t)__float_as_uint(hw) - (int32_t)__float_as_uint(ref);
+    const uint32_t ad = (uint32_t)(d < 0 ? -d : d);
+    worst = max(worst, ad);
+    over1 += ad > 1;
+    over4 += ad > 4;
+  }
+  atomicMax(&out[0], worst);
+  if (over1) atomicAdd(&out[1], over1);
+  if (over4) atomicAdd(&out[2], over4);
+}
+
 void probe_fast_math(pfhip_backend* b, int which, uint32_t lo, uint32_t hi, uint32_t* out) {
   PF_CHECK(lo <= hi, "probe_fast_math: empty range");
   ProfScope ps(b, "probe_fast_math");
   if (which == 0)
     hipLaunchKernelGGL(k_probe_div_one_plus, dim3(8192), dim3(256), 0, b->stream, lo, hi, out);
-  else
+  else if (which == 1)
     hipLaunchKernelGGL(k_probe_exp_fast, dim3(8192), dim3(256), 0, b->stream, lo, hi, out);
+  else
+    hipLaunchKernelGGL(k_probe_exp2_hw, dim3(8192), dim3(256), 0, b->stream, lo, hi, out);
   PF_HIP(hipGetLastError());
 }
 

@@ -194,6 +194,7 @@ struct AttnArgs {
   uint16_t* out; int out_stride;
   int B, T, Hq, Hkv, head_dim, window;
   float scale;
+  int hw_exp;           // 1: hardware exp2 softmax (the GPU paths' numerics); 0: the WASM path's
 };
 void banded_attention(pfhip_backend* b, const AttnArgs& a);
 

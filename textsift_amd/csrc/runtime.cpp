@@ -231,6 +231,8 @@ static std::vector<KernelEntry>& registry() {
                  // reference's unscaled Q.K (attention.ts:139-145).
                  const float sc = pfv(p, 6);
                  a.scale = sc == 0.0f ? 1.0f : sc;
+                 // _pad1 = 1 selects the hardware-exp softmax of the fp16 forward
+                 a.hw_exp = pu(p, 7) == 1;
                  a.B = 1;
                  need(bs, 0, (size_t)a.T * a.Hq * a.head_dim * 2, "banded_attention");
                  need(bs, 1, (size_t)a.T * a.Hkv * a.head_dim * 2, "banded_attention");
