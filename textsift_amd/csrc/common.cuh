@@ -83,6 +83,42 @@ __device__ __forceinline__ float hw_h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
+typedef uint16_t us2_t __attribute__((ext_vector_type(2)));
+
+// True when the four fp16 values packed in w are all normal numbers (no
+// zero, subnormal, inf or NaN): wasm_h2f of each is then the hardware
+// widening. Per half h = bits & 0x7fff: 0x0400 <= h < 0x7c00, tested as
+// (h - 0x0400) mod 2^16 < 0x7800 with packed 16-bit arithmetic.
+__device__ __forceinline__ bool h4_normal(u2_t w) {
+  const us2_t k = {0x0400, 0x0400};
+  const us2_t a = __builtin_bit_cast(us2_t, w.x & 0x7fff7fffu) - k;
+  const us2_t b = __builtin_bit_cast(us2_t, w.y & 0x7fff7fffu) - k;
+  const us2_t m = __builtin_elementwise_max(a, b);
+  return (m.x < 0x7800) & (m.y < 0x7800);
+}
+
+__device__ __noinline__ f4_t h4_widen_exact(u2_t w) {
+  return f4_t{wasm_h2f((uint16_t)(w.x & 0xFFFFu)), wasm_h2f((uint16_t)(w.x >> 16)),
+              wasm_h2f((uint16_t)(w.y & 0xFFFFu)), wasm_h2f((uint16_t)(w.y >> 16))};
+}
+
+// wasm_h2f of four packed fp16 values: the hardware widening when all are
+// normal, the exact software path (not inlined) otherwise.
+__device__ __forceinline__ void h4_widen(u2_t w, float v[4]) {
+  if (h4_normal(w)) {
+    v[0] = hw_h2f((uint16_t)(w.x & 0xFFFFu));
+    v[1] = hw_h2f((uint16_t)(w.x >> 16));
+    v[2] = hw_h2f((uint16_t)(w.y & 0xFFFFu));
+    v[3] = hw_h2f((uint16_t)(w.y >> 16));
+  } else {
+    const f4_t e = h4_widen_exact(w);
+    v[0] = e[0];
+    v[1] = e[1];
+    v[2] = e[2];
+    v[3] = e[3];
+  }
+}
+
 // f32 -> exact (hi, lo) fp16 pair: hi = fp16(v), lo = fp16(v - hi); hi + lo
 // carries 22 significant bits of v (the form SPLIT GEMM inputs take).
 __device__ __forceinline__ void split_hilo(float v, uint16_t& hi, uint16_t& lo) {

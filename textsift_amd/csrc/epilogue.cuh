@@ -50,17 +50,18 @@ __device__ __noinline__ u2_t rope_f16x4_exact(f4_t v, f2_t cs, f2_t sn) {
   return pack4(hb);
 }
 
-// 4 f32 -> 4 fp16 as wasm_f2h rounds.
+// 4 f32 -> 4 fp16 as wasm_f2h rounds. Where every |v| lies in
+// [2^-14, 65504] both round to nearest even and the hardware packed
+// conversion is used (one min/max test over the four values); otherwise
+// (zeros included) the exact software path.
 __device__ __forceinline__ u2_t to_f16x4(const float v[4]) {
-  uint16_t hb[4];
-  bool ok = true;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    hb[r] = hw_f2h(v[r]);
-    ok &= f16_plain(v[r]);  // bitwise: no branch per test
-  }
-  if (!ok) return to_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]});
-  return pack4(hb);
+  const float lo = fminf(fminf(fabsf(v[0]), fabsf(v[1])), fminf(fabsf(v[2]), fabsf(v[3])));
+  const float hi = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  // NaN anywhere makes both comparisons false
+  if (!(lo >= 6.103515625e-05f && hi <= 65504.0f)) return to_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]});
+  const h2_t a = __builtin_convertvector(f2_t{f32_fence(v[0]), f32_fence(v[1])}, h2_t);
+  const h2_t b = __builtin_convertvector(f2_t{f32_fence(v[2]), f32_fence(v[3])}, h2_t);
+  return u2_t{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
 
 // fp16 output of v with the RoPE rotation of pairs (n, n+1), (n+2, n+3)

@@ -53,19 +53,10 @@ constexpr int MAXJ = 4;  // 256-element slices per row
 enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_SPLIT = 2 };
 
 __device__ __forceinline__ void ld4_h2f(const uint16_t* p, float v[4]) {
-  const u2_t w = *reinterpret_cast<const u2_t*>(p);
-  v[0] = wasm_h2f((uint16_t)(w.x & 0xFFFFu));
-  v[1] = wasm_h2f((uint16_t)(w.x >> 16));
-  v[2] = wasm_h2f((uint16_t)(w.y & 0xFFFFu));
-  v[3] = wasm_h2f((uint16_t)(w.y >> 16));
+  h4_widen(*reinterpret_cast<const u2_t*>(p), v);
 }
 
-__device__ __forceinline__ void h4_to_f(u2_t w, float v[4]) {
-  v[0] = wasm_h2f((uint16_t)(w.x & 0xFFFFu));
-  v[1] = wasm_h2f((uint16_t)(w.x >> 16));
-  v[2] = wasm_h2f((uint16_t)(w.y & 0xFFFFu));
-  v[3] = wasm_h2f((uint16_t)(w.y >> 16));
-}
+__device__ __forceinline__ void h4_to_f(u2_t w, float v[4]) { h4_widen(w, v); }
 
 template <int MODE>
 __device__ __forceinline__ void put4(void* out, uint16_t* out_lo, size_t i, const float y[4]) {
