@@ -52,9 +52,6 @@ constexpr int MAXJ = 4;  // 256-element slices per row
 // Output forms of a normalised row: fp16, f32, or the f32 value as hi/lo fp16 planes.
 enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_SPLIT = 2 };
 
-__device__ __forceinline__ void ld4_h2f(const uint16_t* p, float v[4]) {
-  h4_widen(*reinterpret_cast<const u2_t*>(p), v);
-}
 
 __device__ __forceinline__ void h4_to_f(u2_t w, float v[4]) { h4_widen(w, v); }
 
@@ -87,7 +84,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x
   for (int j = 0; j < MAXJ; ++j) {
     const int d = 4 * lane + 256 * j;
     if (d < D) {
-      ld4_h2f(x + base + d, v[j]);
+      h4_to_f(*reinterpret_cast<const u2_t*>(x + base + d), v[j]);
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[j][r] = 0.0f;
@@ -102,7 +99,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x
     const int d = 4 * lane + 256 * j;
     if (d < D) {
       float gm[4], y[4];
-      ld4_h2f(g + d, gm);
+      h4_to_f(*reinterpret_cast<const u2_t*>(g + d), gm);
 #pragma unroll
       for (int r = 0; r < 4; ++r) y[r] = v[j][r] * inv_rms * gm[r];
       put4<MODE>(out, out_lo, base + d, y);
@@ -130,8 +127,8 @@ __global__ __launch_bounds__(256) void k_add_rms_norm(const uint16_t* __restrict
     hs[j] = u2_t{0u, 0u};
     if (d < D) {
       float av[4], bv[4], sv[4];
-      ld4_h2f(a + base + d, av);
-      ld4_h2f(bb + base + d, bv);
+      h4_to_f(*reinterpret_cast<const u2_t*>(a + base + d), av);
+      h4_to_f(*reinterpret_cast<const u2_t*>(bb + base + d), bv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         sv[r] = av[r] + bv[r];
@@ -149,7 +146,7 @@ __global__ __launch_bounds__(256) void k_add_rms_norm(const uint16_t* __restrict
     if (d < D) {
       float hv[4], gm[4], y[4];
       h4_to_f(hs[j], hv);
-      ld4_h2f(g + d, gm);
+      h4_to_f(*reinterpret_cast<const u2_t*>(g + d), gm);
 #pragma unroll
       for (int r = 0; r < 4; ++r) y[r] = hv[r] * inv_rms * gm[r];
       put4<MODE>(norm_out, norm_lo, base + d, y);
@@ -513,31 +510,54 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
 // The reference weights by softmax/K and rescales by K at the end; both are
 // exact powers of two, so weighting by the softmax directly is bit-identical.
 // NMODE: -1 = no norm; OUT_F16 / OUT_SPLIT = form of the next block's norm output.
-template <int NMODE>
+template <int NMODE, int K>
 __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                      const int32_t* __restrict__ slot_of, const float* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
                                                      uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
                                                      const uint16_t* __restrict__ gamma,
                                                      uint16_t* __restrict__ norm_hi, uint16_t* __restrict__ norm_lo,
-                                                     int T, int K, int D, float eps) {
+                                                     int T, int D, float eps) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
-  int ek[MAXK], sk[MAXK];
-  float wk[MAXK];
+  int ek[K], sk[K];
+  float wk[K];
+#pragma unroll
   for (int k = 0; k < K; ++k) {
     ek[k] = idx[(size_t)t * K + k];
     wk[k] = w[(size_t)t * K + k];
     sk[k] = slot_of[(size_t)t * K + k];
   }
-  for (int a = 1; a < K; ++a)  // insertion sort by expert id (ids are distinct)
-    for (int j = a; j > 0 && ek[j] < ek[j - 1]; --j) {
-      int te = ek[j]; ek[j] = ek[j - 1]; ek[j - 1] = te;
-      float tw = wk[j]; wk[j] = wk[j - 1]; wk[j - 1] = tw;
-      int ts = sk[j]; sk[j] = sk[j - 1]; sk[j - 1] = ts;
+  // ascending expert id (ids are distinct): a fixed compare-exchange network
+#pragma unroll
+  for (int a = 1; a < K; ++a)
+#pragma unroll
+    for (int j = a; j > 0; --j) {
+      const bool sw = ek[j] < ek[j - 1];
+      const int e0 = ek[j - 1], e1 = ek[j], s0 = sk[j - 1], s1 = sk[j];
+      const float w0 = wk[j - 1], w1 = wk[j];
+      ek[j - 1] = sw ? e1 : e0;
+      ek[j] = sw ? e0 : e1;
+      sk[j - 1] = sw ? s1 : s0;
+      sk[j] = sw ? s0 : s1;
+      wk[j - 1] = sw ? w1 : w0;
+      wk[j] = sw ? w0 : w1;
     }
   const size_t base = (size_t)t * D;
+  // every load of the row is issued before any is used
+  f4_t yv[MAXJ][K];
+  u2_t rw[MAXJ], gw[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int d = 4 * lane + 256 * j;
+    if (d < D) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) yv[j][k] = *reinterpret_cast<const f4_t*>(y + (size_t)sk[k] * D + d);
+      rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
+      if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
+    }
+  }
   u2_t hs[MAXJ];
   float ss = 0.0f;
 #pragma unroll
@@ -546,16 +566,15 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     hs[j] = u2_t{0u, 0u};
     if (d < D) {
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int k = 0; k < K; ++k) {
-        const f4_t yv = *reinterpret_cast<const f4_t*>(y + (size_t)sk[k] * D + d);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], yv[r], acc[r]);
-      }
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], yv[j][k][r], acc[r]);
       const u2_t m = to_f16x4(acc);
       if (moe_out) *reinterpret_cast<u2_t*>(moe_out + base + d) = m;
       float mv[4], rv[4], sv[4];
       h4_to_f(m, mv);
-      ld4_h2f(residual + base + d, rv);
+      h4_to_f(rw[j], rv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) sv[r] = rv[r] + mv[r];
       hs[j] = to_f16x4(sv);
@@ -574,15 +593,34 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     for (int j = 0; j < MAXJ; ++j) {
       const int d = 4 * lane + 256 * j;
       if (d < D) {
-        float hv[4], gm[4], yv[4];
+        float hv[4], gm[4], yo[4];
         h4_to_f(hs[j], hv);
-        ld4_h2f(gamma + d, gm);
+        h4_to_f(gw[j], gm);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = hv[r] * inv_rms * gm[r];
-        put4<NMODE>(norm_hi, norm_lo, base + d, yv);
+        for (int r = 0; r < 4; ++r) yo[r] = hv[r] * inv_rms * gm[r];
+        put4<NMODE>(norm_hi, norm_lo, base + d, yo);
       }
     }
   }
+}
+
+template <int NMODE>
+void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
+                    const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
+                    uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
+  const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  switch (K) {
+#define PF_COMBINE_CASE(k)                                                                                       \
+  case k:                                                                                                        \
+    hipLaunchKernelGGL((k_moe_combine<NMODE, k>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y, residual,   \
+                       moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);                                      \
+    break;
+    PF_COMBINE_CASE(1) PF_COMBINE_CASE(2) PF_COMBINE_CASE(3) PF_COMBINE_CASE(4)
+    PF_COMBINE_CASE(5) PF_COMBINE_CASE(6) PF_COMBINE_CASE(7) PF_COMBINE_CASE(8)
+#undef PF_COMBINE_CASE
+    default: throw Error("moe_combine: K must be 1..8");
+  }
+  PF_HIP(hipGetLastError());
 }
 
 // ----------------------------------------------------------------------------
@@ -958,27 +996,22 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
 
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                  const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D) {
-  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K <= MAXK, "moe_combine: shape out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K >= 1 && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine");
-  hipLaunchKernelGGL(k_moe_combine<-1>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
-                     moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
-  PF_HIP(hipGetLastError());
+  launch_combine<-1>(b, idx, w, slot_of, y, residual, moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
 }
 
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
                       const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps) {
-  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K <= MAXK, "moe_combine: shape out of range");
+  PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K >= 1 && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine_norm");
   if (norm_lo)
-    hipLaunchKernelGGL(k_moe_combine<OUT_SPLIT>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y,
-                       residual, nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
+    launch_combine<OUT_SPLIT>(b, idx, w, slot_of, y, residual, nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
   else
-    hipLaunchKernelGGL(k_moe_combine<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, idx, w, slot_of, y,
-                       residual, nullptr, h_out, gamma, norm_hi, nullptr, T, K, D, eps);
-  PF_HIP(hipGetLastError());
+    launch_combine<OUT_F16>(b, idx, w, slot_of, y, residual, nullptr, h_out, gamma, norm_hi, nullptr, T, K, D, eps);
 }
 
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
