@@ -180,3 +180,24 @@ def test_detect_spans_vs_oracle(small):
             ok, rep = span_parity(g, r, c)
             print(f"  chunk of {c.token_ids.size} tokens: identical {ok} {rep}")
             assert ok or near_tie_only(rep, c.token_ids.size)
+
+
+def test_forward_from_onnx_file(small, tmp_path):
+    """Weights read from an ONNX q4f16 graph + external data (the real-model
+    load path, native/backend.ts:140-236) give bit-identical logits."""
+    from test_onnx_reader import write_model
+    from textsift_amd.onnx_reader import load_onnx_weights
+
+    w, be = small
+    path = tmp_path / "model_q4f16.onnx"
+    write_model(w, path, num_layers=L)
+    be2 = HipBackend(load_onnx_weights(str(path)), precision=be.precision)
+    be2.warmup()
+    try:
+        ids = synth.token_ids(4242, 300, V)
+        mask = np.ones(300, np.uint8)
+        a = be.forward(ids, mask).data
+        b = be2.forward(ids, mask).data
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        be2.dispose()
