@@ -201,3 +201,53 @@ def test_forward_from_onnx_file(small, tmp_path):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     finally:
         be2.dispose()
+
+
+def test_padded_window_batch_is_exact(small):
+    """Streaming windows of different lengths in one right-padded, masked
+    batched forward: each window's logits equal its own forward's bit for
+    bit (fp16 numerics; masked keys add exact zeros to the softmax)."""
+    from textsift_amd.stream import _forward_windows
+
+    w, be = small
+    if be.precision != _native.PRECISION_FP16:
+        pytest.skip("the split numerics' exp choice depends on the window length")
+    chunks = []
+    for i, n in enumerate((300, 57, 512, 1, 129)):
+        ids = synth.token_ids(5000 + i, n, V)
+        chunks.append(Chunk(ids, np.ones(n, np.uint8), list(range(n + 1)), "x" * n, 0, (0, n)))
+    batched = _forward_windows(be, chunks)
+    for c, got in zip(chunks, batched):
+        alone = be.forward(c.token_ids, c.attention_mask).as_matrix()
+        assert np.array_equal(got.view(np.uint32), alone.view(np.uint32)), c.token_ids.size
+
+
+def test_stream_batcher_on_gpu(small):
+    """Three interleaved streams through the HIP backend, one forward per
+    step, give each stream the spans it gets when run alone."""
+    from parity_util import WordTokenizer, random_words
+    from textsift_amd.stream import DetectStream, StreamBatcher
+
+    w, be = small
+    tok = WordTokenizer(V)
+    dec = ViterbiDecoder(zero_calibration())
+    texts = [random_words(n, 70 + n) for n in (400, 150, 900)]
+    pieces = [[t[i:i + 97] for i in range(0, len(t), 97)] for t in texts]
+    alone = [[(s.label, s.start, s.end) for s in DetectStream(p, be, tok, dec, 256, 64)] for p in pieces]
+    b = StreamBatcher(be, tok, dec, 256, 64)
+    sids = [b.open() for _ in texts]
+    got = {s: [] for s in sids}
+    qs = [list(p) for p in pieces]
+    while any(qs):
+        for s, q in zip(sids, qs):
+            if q:
+                b.feed(s, q.pop(0))
+        for s, spans in b.step().items():
+            got[s] += [(x.label, x.start, x.end) for x in spans]
+    for s in sids:
+        got[s] += [(x.label, x.start, x.end) for x in b.finish(s)]
+    exact = be.precision == _native.PRECISION_FP16
+    for s, ref in zip(sids, alone):
+        print(f"stream {s}: {len(ref)} spans, identical {got[s] == ref}")
+        if exact:
+            assert got[s] == ref
