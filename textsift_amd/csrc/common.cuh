@@ -209,19 +209,19 @@ __device__ __forceinline__ float swiglu_clamp_fast(float gate_raw, float up_raw)
 }
 
 // SwiGLU with the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; each
-// within about 1 ulp), in the form of the reference's GPU shader
-// (src/native/shaders/swiglu_clamp.wgsl:10-25): sigma(x) = 1 / (1 + exp(-x))
-// for x >= 0, else e / (1 + e) with e = exp(x). Used by the fp16 forward,
-// which follows the GPU paths' numerics; it differs from swiglu_clamp by a
-// few f32 ulps, which changes an fp16-rounded output in about one case in a
-// thousand, by one fp16 ulp.
+// within about 1 ulp), for the fp16 forward, which follows the GPU paths'
+// numerics (src/native/shaders/swiglu_clamp.wgsl:10-25 uses the WGSL exp).
+// sigma(x) = 1 / (1 + exp(-x)) needs no branch here: for very negative x the
+// hardware exp2 returns +inf and its reciprocal 0. alpha * log2(e) is folded
+// into one constant. The result differs from swiglu_clamp by a few f32 ulps,
+// which changes an fp16-rounded output in about one case in a thousand, by
+// one fp16 ulp (plus the reference polynomial's own error, ~1e-4 relative,
+// which the GPU paths do not have).
 __device__ __forceinline__ float swiglu_clamp_hw(float gate_raw, float up_raw) {
   const float gate = fminf(gate_raw, 7.0f);
-  const float up = fmaxf(fminf(up_raw, 7.0f), -7.0f);
-  const float x = gate * 1.702f;
-  const float e = __builtin_amdgcn_exp2f(-fabsf(x) * 1.44269504088896340736f);
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);
-  const float sig = x >= 0.0f ? r : e * r;
+  const float up = __builtin_amdgcn_fmed3f(up_raw, -7.0f, 7.0f);
+  constexpr float NEG_ALPHA_LOG2E = -1.702f * 1.44269504088896340736f;
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gate * NEG_ALPHA_LOG2E));
   return (up + 1.0f) * (gate * sig);
 }
 

@@ -80,6 +80,27 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
   return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
 }
 
+// Geometry of the LDS-staged output of a (WF, BT) tile: ESZ output bytes per
+// element, CF output columns per 16-row fragment, FB bytes per row of one
+// fragment, PS bytes one lane holds per fragment row; the tile is staged in
+// NP passes of FG fragments per wave (PRB bytes per staged row, UP 16-byte
+// units, units XOR-swizzled by row & SWM for conflict-free LDS writes).
+template <int WF, int BT, Epi EPI>
+struct StagedOut {
+  static constexpr bool OK = EPI == Epi::F32 || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16;
+  static constexpr int ESZ = EPI == Epi::F32 ? 4 : 2;
+  static constexpr int CF = EPI == Epi::SWIGLU_F16 ? 8 : 16;
+  static constexpr int FB = CF * ESZ;
+  static constexpr int PS = FB / 4;
+  static constexpr int NP = (NW * WF * FB * BT > 65536 && WF % 2 == 0) ? 2 : 1;
+  static constexpr int FG = WF / NP;
+  static constexpr int PRB = NW * FG * FB;
+  static constexpr int UP = PRB / 16;
+  static constexpr int SWM = UP % 16 == 0 ? 15 : (UP % 8 == 0 ? 7 : (UP % 4 == 0 ? 3 : 0));
+  static constexpr size_t LDS = (size_t)BT * PRB;
+  static_assert(BT * UP % 256 == 0, "staged stores: whole rounds of 256 units");
+};
+
 template <int WF, int BT, int XS, Epi EPI, bool GROUPED>
 __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
@@ -162,11 +183,43 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
     }
   };
 
+  // The accumulators start at the bias of the lane's 4 columns of each
+  // fragment (the MFMAs add onto it); columns past N get 0 and are never
+  // stored. Loads are unconditional (indices clamped).
+  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
+  int ncol[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * WF + f) * 16 + 4 * lg;
   f4_t acc[WF][TJ];
+  {
+    u2_t braw[WF];
 #pragma unroll
-  for (int f = 0; f < WF; ++f)
+    for (int f = 0; f < WF; ++f) braw[f] = u2_t{0u, 0u};
+    if (BIAS) {
+      if ((p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(BIAS) & 7) == 0) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+        for (int f = 0; f < WF; ++f) braw[f] = *reinterpret_cast<const u2_t*>(BIAS + min(ncol[f], p.N - 4));
+      } else {
+#pragma unroll
+        for (int f = 0; f < WF; ++f) {
+          uint32_t h[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) h[r] = BIAS[min(ncol[f] + r, p.N - 1)];
+          braw[f] = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      const uint32_t bw[2] = {braw[f].x, braw[f].y};
+      float bv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        bv[r] = ncol[f] + r < p.N ? wasm_h2f((uint16_t)(bw[r >> 1] >> (16 * (r & 1)))) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
+    }
+  }
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
   auto compute = [&](int buf) {
@@ -216,32 +269,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  // ---- epilogue operands, loaded before the last chunk's MFMAs so that their
-  // latency overlaps them: the bias of the lane's 4 columns of every fragment
-  // and, for RoPE, the table entries of the first fragment's rows. Every load
-  // is unconditional (indices clamped); columns and rows past the edges are
-  // never stored.
-  const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
-  int ncol[WF];
-#pragma unroll
-  for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * WF + f) * 16 + 4 * lg;
-  u2_t braw[WF];
-#pragma unroll
-  for (int f = 0; f < WF; ++f) braw[f] = u2_t{0u, 0u};
-  if (BIAS) {
-    if ((p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(BIAS) & 7) == 0) {
-#pragma unroll
-      for (int f = 0; f < WF; ++f) braw[f] = *reinterpret_cast<const u2_t*>(BIAS + min(ncol[f], p.N - 4));
-    } else {
-#pragma unroll
-      for (int f = 0; f < WF; ++f) {
-        uint32_t h[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h[r] = BIAS[min(ncol[f] + r, p.N - 1)];
-        braw[f] = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      }
-    }
-  }
+  // ---- RoPE operands, loaded before the last chunk's MFMAs so that their
+  // latency overlaps them.
   // RoPE: the table rows (32 cos + 32 sin f32 = 256 bytes, the size of an
   // activation row) of the tile's BT positions are copied into the LDS buffer
   // the last chunk does not use, swizzled like the activations so that the
@@ -269,14 +298,77 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
   }
 
   // ---- epilogue: lane holds out[token = 16 tj + l16][n = n0 + (wave WF + f) 16 + 4 lg + r]
+  using SO = StagedOut<WF, BT, EPI>;
+  if (SO::OK && p.out_staged) {
+    // The tile goes out through LDS: lanes write their values in row-major
+    // order, then every lane stores whole 16-byte units of consecutive
+    // columns, so each row segment of the tile leaves as full lines (the
+    // direct form writes 4- to 16-byte pieces of 16 rows per instruction,
+    // which costs the gate_up GEMM about a fifth of its time).
+    char* ob = reinterpret_cast<char*>(xs_lds);
+    u2_t ow[WF][TJ];  // packed fp16 results (F32 writes the accumulators)
+    if constexpr (EPI != Epi::F32) {
+#pragma unroll
+      for (int f = 0; f < WF; ++f) {
+        const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
+        const int pidx = (ncol[f] & 63) >> 1;
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj) {
+          const float v[4] = {acc[f][tj][0], acc[f][tj][1], acc[f][tj][2], acc[f][tj][3]};
+          if constexpr (EPI == Epi::ROPE_F16) {
+            if (rope) {
+              const char* trow = reinterpret_cast<const char*>(xs_lds + (C & 1) * XS * PLANE) + (16 * tj + l16) * 256;
+              const int ucs = (pidx >> 2) ^ l16, usn = ((pidx >> 2) + 8) ^ l16;
+              const f2_t cs = *reinterpret_cast<const f2_t*>(trow + ucs * 16 + (pidx & 3) * 4);
+              const f2_t sn = *reinterpret_cast<const f2_t*>(trow + usn * 16 + (pidx & 3) * 4);
+              ow[f][tj] = rope_f16x4(v, cs, sn);
+            } else {
+              ow[f][tj] = to_f16x4(v);
+            }
+          } else if constexpr (EPI == Epi::F16) {
+            ow[f][tj] = to_f16x4(v);
+          } else {
+            ow[f][tj] = u2_t{swiglu_f16x2(v), 0u};
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int ps = 0; ps < SO::NP; ++ps) {
+      __syncthreads();  // every wave is done with the LDS buffers (and the previous pass)
+#pragma unroll
+      for (int fl = 0; fl < SO::FG; ++fl) {
+        const int f = ps * SO::FG + fl;
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj) {
+          const int row = 16 * tj + l16;
+          const int byte = (wave * SO::FG + fl) * SO::FB + lg * SO::PS;
+          char* dst = ob + row * SO::PRB + (((byte >> 4) ^ (row & SO::SWM)) << 4) + (byte & 15);
+          if constexpr (EPI == Epi::F32) *reinterpret_cast<f4_t*>(dst) = acc[f][tj];
+          else if constexpr (EPI == Epi::SWIGLU_F16) *reinterpret_cast<uint32_t*>(dst) = ow[f][tj].x;
+          else *reinterpret_cast<u2_t*>(dst) = ow[f][tj];
+        }
+      }
+      __syncthreads();
+      const int ocol0 = EPI == Epi::SWIGLU_F16 ? n0 / 2 : n0;
+      const int oN = EPI == Epi::SWIGLU_F16 ? p.N / 2 : p.N;
+#pragma unroll
+      for (int i = 0; i < BT * SO::UP / 256; ++i) {
+        const int idx = i * 256 + tid, row = idx / SO::UP, up = idx % SO::UP;
+        const int byte = ((up ^ (row & SO::SWM)) << 4);
+        const int w = byte / (SO::FG * SO::FB), within = byte % (SO::FG * SO::FB);
+        const int col = ocol0 + (w * WF + ps * SO::FG) * SO::CF + within / SO::ESZ;
+        if (row < rows && col < oN)
+          *reinterpret_cast<u4_t*>(static_cast<char*>(p.out) + ((size_t)(row0 + row) * p.ldo + col) * SO::ESZ) =
+              *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
     const int n = ncol[f];
     if (n >= p.N) continue;
-    const uint32_t bw[2] = {braw[f].x, braw[f].y};
-    float bv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) bv[r] = n + r < p.N ? wasm_h2f((uint16_t)(bw[r >> 1] >> (16 * (r & 1)))) : 0.0f;
     // a fragment of 16 columns lies wholly below or above rope_cols (a multiple of 64)
     const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
     const int pidx = (n & 63) >> 1;  // this lane's first (cos, sin) pair of the head
@@ -287,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
       const size_t orow = (size_t)(row0 + lt);
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[f][tj][r] + bv[r];
+      for (int r = 0; r < 4; ++r) v[r] = acc[f][tj][r];
       if constexpr (EPI == Epi::ROPE_F16) {
         u2_t hv;
         if (rope) {
@@ -315,7 +407,8 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   const long grid = (long)n_tiles * t_tiles;
   if (grid == 0) return;
   PF_CHECK(grid < (1L << 31), "gemm_w4: grid too large");
-  const size_t lds = (size_t)2 * XS * BT * KC * sizeof(uint16_t);
+  const size_t lds = std::max((size_t)2 * XS * BT * KC * sizeof(uint16_t),
+                              StagedOut<WF, BT, EPI>::OK ? StagedOut<WF, BT, EPI>::LDS : (size_t)0);
   static bool attr_set = false;  // per template instance
   if (!attr_set) {
     PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED>),
@@ -401,11 +494,21 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_w4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_w4: M must be non-negative");
   PF_CHECK(xk == XKind::F16, "gemm_w4: activations must be one fp16 plane");
+  // staged (whole-line) output stores need 16-byte aligned rows and no
+  // partial 16-byte unit at column N
+  GemmArgs g = a;
+  {
+    const int esz = epi == Epi::F32 ? 4 : 2;
+    const int ocols = epi == Epi::SWIGLU_F16 ? a.N / 2 : a.N;
+    g.out_staged = (epi == Epi::F32 || epi == Epi::F16 || epi == Epi::ROPE_F16 || epi == Epi::SWIGLU_F16) &&
+                   ocols % (16 / esz) == 0 && (a.ldo * esz) % 16 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && (epi != Epi::SWIGLU_F16 || a.N % 16 == 0);
+  }
   PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
-  if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, a, epi, grouped, prof_name);
-  if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, a, epi, grouped, prof_name);
-  if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, a, epi, grouped, prof_name);
-  if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, a, epi, grouped, prof_name);
+  if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
+  if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
+  if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);
+  if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, g, epi, grouped, prof_name);
   throw Error("gemm_w4: unsupported (tile_t, wf) = (" + std::to_string(tile_t) + ", " + std::to_string(wf) + ")");
 }
 

@@ -115,6 +115,9 @@ struct GemmArgs {
   const float* rope_sin = nullptr;  // wasm_h2f widens them (zig/math.zig:45-52)
   int seq_len = 0;
   int rope_cols = 0;                   // columns [0, rope_cols) are rotated
+  // gemm_w4: stage the output tile through LDS and store whole 16-byte units
+  // (set by gemm_w4 itself when the output layout allows it)
+  int out_staged = 0;
 };
 
 void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
