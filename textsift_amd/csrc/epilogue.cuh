@@ -92,6 +92,30 @@ __device__ __forceinline__ u2_t rope_f16x4(const float v[4], f2_t cs, f2_t sn) {
   return pack4(hb);
 }
 
+// RoPE as the reference's GPU shader computes it (native/shaders/
+// rope_apply.wgsl:26-36): the GEMM result rounded to fp16, then fp16
+// arithmetic throughout, each product and the sum rounded to fp16
+// (v_pk_mul_f16 / v_pk_add_f16, round to nearest even, fp16 subnormals
+// kept). t = {cos, sin} of pair (n, n+1), then of pair (n+2, n+3), as fp16.
+// For normal fp16 values this equals the three-rounding WASM form bit for
+// bit (f32 carries more than 2 x 11 + 2 bits, so rounding a difference of
+// two fp16 values to f32 and then to fp16 equals rounding it once); the two
+// differ only where a product or result is subnormal, which the WASM
+// helpers flush to zero.
+__device__ __forceinline__ u2_t rope_f16x4_native(const float v[4], h4_t t) {
+  const h2_t x[2] = {__builtin_convertvector(f2_t{f32_fence(v[0]), f32_fence(v[1])}, h2_t),
+                     __builtin_convertvector(f2_t{f32_fence(v[2]), f32_fence(v[3])}, h2_t)};
+  uint32_t out[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const _Float16 c = t[2 * h], s = t[2 * h + 1];
+    const h2_t p = x[h] * h2_t{c, c};                  // {a c, b c}
+    const h2_t q = h2_t{x[h][1], x[h][0]} * h2_t{s, s};  // {b s, a s}
+    out[h] = __builtin_bit_cast(uint32_t, p + h2_t{-q[0], q[1]});
+  }
+  return u2_t{out[0], out[1]};
+}
+
 // Stores 4 packed fp16 values at out[orow][n..n+3] (columns past N dropped).
 __device__ __forceinline__ void store_f16x4(const GemmArgs& p, size_t orow, int n, u2_t hv) {
   uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;

@@ -84,6 +84,7 @@ struct pfhip_model {
   int rope_T = 0;
   float* rope_cos = nullptr;  // fp16 table entries, widened as the reference widens them
   float* rope_sin = nullptr;
+  uint16_t* rope_pairs = nullptr;  // [T][hd/2][cos, sin] fp16 bits (fp16 numerics)
   // host-API staging
   pfhip_buffer* ids_buf = nullptr;
   pfhip_buffer* mask_buf = nullptr;
@@ -292,17 +293,24 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       PF_HIP(hipStreamSynchronize(b->stream));
       hipFree(m->rope_cos);
       hipFree(m->rope_sin);
+      hipFree(m->rope_pairs);
       m->rope_cos = m->rope_sin = nullptr;
+      m->rope_pairs = nullptr;
     }
     std::vector<float> csf(cs.size()), snf(sn.size());
+    std::vector<uint16_t> pairs(2 * cs.size());
     for (size_t i = 0; i < cs.size(); ++i) {
       csf[i] = wasm_h2f_host(cs[i]);
       snf[i] = wasm_h2f_host(sn[i]);
+      pairs[2 * i] = cs[i];
+      pairs[2 * i + 1] = sn[i];
     }
     PF_HIP(hipMalloc(&m->rope_cos, csf.size() * 4));
     PF_HIP(hipMalloc(&m->rope_sin, snf.size() * 4));
+    PF_HIP(hipMalloc(&m->rope_pairs, pairs.size() * 2));
     PF_HIP(hipMemcpy(m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice));
     PF_HIP(hipMemcpy(m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice));
+    PF_HIP(hipMemcpy(m->rope_pairs, pairs.data(), pairs.size() * 2, hipMemcpyHostToDevice));
     m->rope_T = T;
   }
 
@@ -324,7 +332,8 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
       a.w = L.qkv.q; a.ws = L.qkv.s; a.wz = L.qkv.z; a.bias = L.qkv.bias;
       a.out = s.qkv; a.ldo = NQKV; a.M = M; a.N = NQKV; a.K = D;
-      a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
+      a.rope_cos = m->rope_cos; a.rope_sin = m->rope_sin; a.rope_pairs = m->rope_pairs;
+      a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.qkv4.w); a.wsz = L.qkv4.sz;
         gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, 128, 2, "gemm_qkv_rope");  // N = 1152 = 9 x 128
@@ -485,6 +494,7 @@ void pfhip_model_destroy(pfhip_model* m) {
   if (m->scratch) hipFree(m->scratch);
   if (m->rope_cos) hipFree(m->rope_cos);
   if (m->rope_sin) hipFree(m->rope_sin);
+  if (m->rope_pairs) hipFree(m->rope_pairs);
   pfhip_release_buffer(m->b, m->ids_buf);
   pfhip_release_buffer(m->b, m->mask_buf);
   pfhip_release_buffer(m->b, m->logits_buf);

@@ -57,6 +57,13 @@ __device__ __forceinline__ void copy16_to_lds(const void* src, lds_ptr_t dst) {
 
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
+// {cos, sin} of pairs pidx and pidx + 1 (pidx even) from row `row` of the
+// LDS-staged RoPE table (128-byte rows, units swizzled by row & 7).
+__device__ __forceinline__ h4_t rope_entry(const _Float16* tb, int row, int pidx) {
+  const char* trow = reinterpret_cast<const char*>(tb) + row * 128;
+  return *reinterpret_cast<const h4_t*>(trow + (((pidx >> 2) ^ (row & 7)) << 4) + (pidx & 3) * 4);
+}
+
 // One repacked dword (8 nibbles) -> fp16 (q - zp) * scale for k = 0..7.
 // off = (-(1024 + zp), -(1024 + zp)), sc = (scale, scale).
 __device__ __forceinline__ h8_t dequant_fold(uint32_t w, h2_t off, h2_t sc) {
@@ -271,23 +278,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
 
   // ---- RoPE operands, loaded before the last chunk's MFMAs so that their
   // latency overlaps them.
-  // RoPE: the table rows (32 cos + 32 sin f32 = 256 bytes, the size of an
-  // activation row) of the tile's BT positions are copied into the LDS buffer
-  // the last chunk does not use, swizzled like the activations so that the
-  // epilogue's reads are conflict-free. Row r of the tile is at position
-  // (row0 + r) mod seq_len.
+  // RoPE: the table rows (32 (cos, sin) fp16 pairs = 128 bytes) of the
+  // tile's BT positions are copied into the LDS buffer the last chunk does
+  // not use, their eight 16-byte units XOR-swizzled by (row & 7). Row r of
+  // the tile is at position (row0 + r) mod seq_len. One wave instruction
+  // fills 8 rows.
   if constexpr (EPI == Epi::ROPE_F16) {
+    static_assert(BT % (8 * NW) == 0, "RoPE table staging: whole rounds of 8 rows per wave");
     const int p0 = (int)((uint32_t)row0 % (uint32_t)p.seq_len);
     _Float16* tb = xs_lds + (C & 1) * XS * PLANE;
 #pragma unroll
-    for (int m = 0; m < XI; ++m) {
-      const int r = (m * NW + wave) * 4 + lg;
+    for (int m = 0; m < BT / (8 * NW); ++m) {
+      const int r = (m * NW + wave) * 8 + (lane >> 3);
       int q = p0 + r;
       if (p.seq_len >= BT) q = q >= p.seq_len ? q - p.seq_len : q;
       else q %= p.seq_len;
-      const int u = l16 ^ (r & 15);  // this lane's 16-byte unit lands at position l16 of row r
-      const float* src = (u < 8 ? p.rope_cos + u * 4 : p.rope_sin + (u - 8) * 4) + (size_t)q * 32;
-      copy16_to_lds(src, (lds_ptr_t)(tb + (m * NW + wave) * 512));
+      const int u = (lane & 7) ^ (r & 7);  // this lane's unit lands at position lane & 7 of row r
+      copy16_to_lds(p.rope_pairs + (size_t)q * 64 + u * 8, (lds_ptr_t)(tb + (m * NW + wave) * 512));
     }
   }
 
@@ -317,11 +324,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
           const float v[4] = {acc[f][tj][0], acc[f][tj][1], acc[f][tj][2], acc[f][tj][3]};
           if constexpr (EPI == Epi::ROPE_F16) {
             if (rope) {
-              const char* trow = reinterpret_cast<const char*>(xs_lds + (C & 1) * XS * PLANE) + (16 * tj + l16) * 256;
-              const int ucs = (pidx >> 2) ^ l16, usn = ((pidx >> 2) + 8) ^ l16;
-              const f2_t cs = *reinterpret_cast<const f2_t*>(trow + ucs * 16 + (pidx & 3) * 4);
-              const f2_t sn = *reinterpret_cast<const f2_t*>(trow + usn * 16 + (pidx & 3) * 4);
-              ow[f][tj] = rope_f16x4(v, cs, sn);
+              const int row = 16 * tj + l16;
+              ow[f][tj] = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, row, pidx));
             } else {
               ow[f][tj] = to_f16x4(v);
             }
@@ -383,11 +387,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
       if constexpr (EPI == Epi::ROPE_F16) {
         u2_t hv;
         if (rope) {
-          const char* trow = reinterpret_cast<const char*>(xs_lds + (C & 1) * XS * PLANE) + lt * 256;
-          const int ucs = (pidx >> 2) ^ l16, usn = ((pidx >> 2) + 8) ^ l16;  // row lt: (lt & 15) == l16
-          const f2_t cs = *reinterpret_cast<const f2_t*>(trow + ucs * 16 + (pidx & 3) * 4);
-          const f2_t sn = *reinterpret_cast<const f2_t*>(trow + usn * 16 + (pidx & 3) * 4);
-          hv = rope_f16x4(v, cs, sn);
+          hv = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, lt, pidx));
         } else {
           hv = to_f16x4(v);
         }
@@ -488,8 +488,9 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   if (epi == Epi::SWIGLU_SPLIT || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_w4: SwiGLU needs N % 4 == 0");
   if (epi == Epi::SWIGLU_SPLIT) PF_CHECK(a.out_lo, "gemm_w4: SWIGLU_SPLIT needs an output lo plane");
   if (epi == Epi::ROPE_F16)
-    PF_CHECK(a.rope_cos && a.rope_sin && a.seq_len > 0 && a.rope_cols % 64 == 0,
-             "gemm_w4: RoPE epilogue needs tables, seq_len and head-aligned rope_cols");
+    PF_CHECK(a.rope_pairs && (reinterpret_cast<uintptr_t>(a.rope_pairs) & 15) == 0 && a.seq_len > 0 &&
+                 a.rope_cols % 64 == 0,
+             "gemm_w4: RoPE epilogue needs an aligned fp16 pair table, seq_len and head-aligned rope_cols");
   if (epi == Epi::ROPE_F16) PF_CHECK(!grouped && (long)a.M < (1L << 31), "RoPE epilogue: dense rows below 2^31");
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_w4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_w4: M must be non-negative");

@@ -113,6 +113,7 @@ struct GemmArgs {
   // RoPE epilogue
   const float* rope_cos = nullptr;  // [seq_len][head_dim/2]: fp16 table entries widened as
   const float* rope_sin = nullptr;  // wasm_h2f widens them (zig/math.zig:45-52)
+  const uint16_t* rope_pairs = nullptr;  // [seq_len][head_dim/2][cos, sin] fp16 bits (gemm_w4)
   int seq_len = 0;
   int rope_cols = 0;                   // columns [0, rope_cols) are rotated
   // gemm_w4: stage the output tile through LDS and store whole 16-byte units
