@@ -52,7 +52,8 @@ __device__ __forceinline__ int wave_max_i(int v) {
 // ulp) on scores pre-multiplied by log2(e), as the reference's GPU shader
 // uses the WGSL exp (src/native/shaders/banded_attention.wgsl:100-113);
 // otherwise they follow the WASM path (polynomial expApprox for the 4-lane
-// part, libm exp for the scalar tail).
+// part, libm exp for the scalar tail). HWX also stores the output with the
+// hardware fp16 conversion (subnormals kept) as the shader's f16 store does.
 template <int HD, int NCH, int NW, bool HWX>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   constexpr int QB = 16 * NW;                // query tokens per workgroup
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const float ov[4] = {o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
-        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = to_f16x4(ov);
+        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = HWX ? to_f16x4_native(ov) : to_f16x4(ov);
       }
     }
   }

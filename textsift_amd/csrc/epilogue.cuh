@@ -1,10 +1,12 @@
 // epilogue.cuh — output stage shared by the int4 GEMM kernels.
 //
 // A lane holds 4 consecutive output columns n..n+3 of one output row (the
-// GEMMs are computed transposed). The conversions to fp16 follow the
-// reference (zig/math.zig:45-82) bit for bit; the cheap hardware conversion
-// is used where the two agree (f16_plain) and the exact software path only
-// for lanes where they may not.
+// GEMMs are computed transposed). The split numerics' conversions to fp16
+// follow the WASM path (zig/math.zig:45-82) bit for bit; the cheap hardware
+// conversion is used where the two agree (f16_plain) and the exact software
+// path only for lanes where they may not. The fp16 numerics use the
+// `_native` forms: the hardware conversions and fp16 arithmetic the
+// reference's GPU shaders perform.
 #pragma once
 #include "common.cuh"
 #include "pfhip_internal.h"
@@ -137,6 +139,21 @@ __device__ __forceinline__ uint32_t swiglu_f16x2(const float v[4]) {
   const float g1 = swiglu_clamp_hw(v[2], v[3]);
   if (!(fabsf(g0) >= 6.103515625e-05f && fabsf(g1) >= 6.103515625e-05f))
     return to_f16x4_exact(f4_t{g0, g1, 0.f, 0.f}).x;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{f32_fence(g0), f32_fence(g1)}, h2_t));
+}
+
+// The conversions of the GPU shaders' fp16 stores (hardware round to
+// nearest even, fp16 subnormals kept), used by the fp16 numerics. They
+// differ from wasm_f2h only for results below 2^-14 in magnitude (which the
+// WASM helpers flush to zero) and in NaN payloads.
+__device__ __forceinline__ u2_t to_f16x4_native(const float v[4]) {
+  const h2_t a = __builtin_convertvector(f2_t{f32_fence(v[0]), f32_fence(v[1])}, h2_t);
+  const h2_t b = __builtin_convertvector(f2_t{f32_fence(v[2]), f32_fence(v[3])}, h2_t);
+  return u2_t{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+__device__ __forceinline__ uint32_t swiglu_f16x2_native(const float v[4]) {
+  const float g0 = swiglu_clamp_hw(v[0], v[1]);
+  const float g1 = swiglu_clamp_hw(v[2], v[3]);
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{f32_fence(g0), f32_fence(g1)}, h2_t));
 }
 

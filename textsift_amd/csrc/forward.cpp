@@ -336,7 +336,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.qkv4.w); a.wsz = L.qkv4.sz;
-        gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, 128, 2, "gemm_qkv_rope");  // N = 1152 = 9 x 128
+        gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, 128, 4, "gemm_qkv_rope");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
       }

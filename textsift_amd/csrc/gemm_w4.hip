@@ -327,12 +327,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
               const int row = 16 * tj + l16;
               ow[f][tj] = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, row, pidx));
             } else {
-              ow[f][tj] = to_f16x4(v);
+              ow[f][tj] = to_f16x4_native(v);
             }
           } else if constexpr (EPI == Epi::F16) {
-            ow[f][tj] = to_f16x4(v);
+            ow[f][tj] = to_f16x4_native(v);
           } else {
-            ow[f][tj] = u2_t{swiglu_f16x2(v), 0u};
+            ow[f][tj] = u2_t{swiglu_f16x2_native(v), 0u};
           }
         }
       }
@@ -389,9 +389,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
         if (rope) {
           hv = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, lt, pidx));
         } else {
-          hv = to_f16x4(v);
+          hv = to_f16x4_native(v);
         }
         store_f16x4(p, orow, n, hv);
+      } else if constexpr (EPI == Epi::F16) {
+        store_f16x4(p, orow, n, to_f16x4_native(v));
+      } else if constexpr (EPI == Epi::SWIGLU_F16) {
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + (n >> 1)) =
+            swiglu_f16x2_native(v);
       } else {
         store_out<EPI>(p, orow, n, v);
       }
