@@ -47,14 +47,43 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
-// NW waves x 16 queries per workgroup; NCH 32-key chunks per 16-query tile.
-// HWX: the softmax exponentials use the hardware exp2 (v_exp_f32, about 1
-// ulp) on scores pre-multiplied by log2(e), as the reference's GPU shader
-// uses the WGSL exp (src/native/shaders/banded_attention.wgsl:100-113);
-// otherwise they follow the WASM path (polynomial expApprox for the 4-lane
-// part, libm exp for the scalar tail). HWX also stores the output with the
-// hardware fp16 conversion (subnormals kept) as the shader's f16 store does.
-template <int HD, int NCH, int NW, bool HWX>
+// Stages the workgroup's keys kbase .. kbase + ROWS - 1 of kv head g: K
+// row-major [ROWS][HD + 8], V transposed [HD][ROWS + 8]; rows outside
+// [0, T) are zero (their scores are masked).
+template <int HD, int ROWS, int NT>
+__device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float16* Vt, size_t seq0, int g, int kbase,
+                                         int tid) {
+  constexpr int LDK = HD + 8, LDV = ROWS + 8;
+  static_assert(ROWS % 4 == 0, "V^T staging writes 4 keys at a time");
+  const int T = a.T;
+  for (int i = tid; i < ROWS * (HD / 8); i += NT) {
+    const int r = i / (HD / 8), c = i % (HD / 8);
+    const int key = kbase + r;
+    u4_t kv = {0u, 0u, 0u, 0u};
+    if (key >= 0 && key < T) kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
+    *reinterpret_cast<u4_t*>(&Ks[r * LDK + c * 8]) = kv;
+  }
+  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += NT) {  // 4 keys x 8 dims per thread
+    const int r4 = (i / (HD / 8)) * 4, c = i % (HD / 8);
+    h8_t vh[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key = kbase + r4 + u;
+      u4_t vv = {0u, 0u, 0u, 0u};
+      if (key >= 0 && key < T) vv = *reinterpret_cast<const u4_t*>(a.v + (seq0 + key) * a.v_stride + g * HD + c * 8);
+      vh[u] = __builtin_bit_cast(h8_t, vv);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<h4_t*>(&Vt[(c * 8 + j) * LDV + r4]) = h4_t{vh[0][j], vh[1][j], vh[2][j], vh[3][j]};
+  }
+}
+
+// The WASM path's numerics (split): polynomial expApprox for the
+// reference's 4-lane part, libm exp for its scalar tail, p normalised before
+// P.V. NW waves x 16 queries per workgroup; NCH 32-key chunks per 16-query
+// tile.
+template <int HD, int NCH, int NW>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   constexpr int QB = 16 * NW;                // query tokens per workgroup
   constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
@@ -76,28 +105,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const size_t seq0 = (size_t)bseq * T;
   const int kbase = t0 - W;                  // key index of staged row 0
 
-  // ---- stage K (row-major) and V^T; rows outside [0, T) are zero (masked later)
-  for (int i = tid; i < ROWS * (HD / 8); i += 64 * NW) {
-    const int r = i / (HD / 8), c = i % (HD / 8);
-    const int key = kbase + r;
-    u4_t kv = {0u, 0u, 0u, 0u};
-    if (key >= 0 && key < T) kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
-    *reinterpret_cast<u4_t*>(&Ks[r * LDK + c * 8]) = kv;
-  }
-  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += 64 * NW) {  // 4 keys x 8 dims per thread
-    const int r4 = (i / (HD / 8)) * 4, c = i % (HD / 8);
-    h8_t vh[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key = kbase + r4 + u;
-      u4_t vv = {0u, 0u, 0u, 0u};
-      if (key >= 0 && key < T) vv = *reinterpret_cast<const u4_t*>(a.v + (seq0 + key) * a.v_stride + g * HD + c * 8);
-      vh[u] = __builtin_bit_cast(h8_t, vv);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<h4_t*>(&Vt[(c * 8 + j) * LDV + r4]) = h4_t{vh[0][j], vh[1][j], vh[2][j], vh[3][j]};
-  }
+  stage_kv<HD, ROWS, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
   __syncthreads();
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
@@ -118,8 +126,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int any_hi = wave_max_i(q_ok ? hi0 : 0);
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
-  constexpr float LOG2_E = 1.44269504088896340736f;
-  const float sscale = HWX ? a.scale * LOG2_E : a.scale;  // scores in the exponent's units
+  const float sscale = a.scale;
 
   for (int hh = 0; hh < G; ++hh) {
     const int hq = g * G + hh;
@@ -136,7 +143,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
       if (q_ok) v = *reinterpret_cast<const u4_t*>(a.q + (seq0 + tq) * a.q_stride + hq * HD + 32 * dh + 8 * lg);
       qf[dh] = __builtin_bit_cast(h8_t, v);
     }
-    const float sink = a.sinks ? (HWX ? a.sinks[hq] * LOG2_E : a.sinks[hq]) : -INFINITY;
+    const float sink = a.sinks ? a.sinks[hq] : -INFINITY;
 
     // ---- pass 1: scores for the whole band, kept in registers. Slots
     // outside the query's window hold NaN; masked keys hold -inf.
@@ -191,13 +198,13 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const bool plain = !masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi &&
-                         (HWX || !(32 * c + 32 > tail_lo && 32 * c < any_hi));
+                         !(32 * c + 32 > tail_lo && 32 * c < any_hi);
       if (plain) {  // wave-uniform: every slot in every window, no tail key
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float e = HWX ? __builtin_amdgcn_exp2f(s[c][kt][r] - m) : exp_approx_fast(s[c][kt][r] - m);
+            const float e = exp_approx_fast(s[c][kt][r] - m);
             s[c][kt][r] = e;
             l += e;
           }
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
             const float sv = s[c][kt][r];
             const float x = sv - m;
             const int off = 32 * c + 16 * kt + 4 * lg + r;
-            float e = HWX ? __builtin_amdgcn_exp2f(x) : (off >= tail ? expf(x) : exp_approx_fast(x));
+            float e = off >= tail ? expf(x) : exp_approx_fast(x);
             e = (sv != sv) ? 0.0f : e;
             s[c][kt][r] = e;
             l += e;
@@ -219,8 +226,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
     }
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    if constexpr (HWX) l += __builtin_amdgcn_exp2f(sink - m);
-    else l += n_keys < vec_end ? exp_approx_fast(sink - m) : expf(sink - m);
+    l += n_keys < vec_end ? exp_approx_fast(sink - m) : expf(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 
     // ---- pass 3: O^T = V^T . P^T with P normalised, as fp16 hi + lo
@@ -257,32 +263,229 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const float ov[4] = {o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
-        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = HWX ? to_f16x4_native(ov) : to_f16x4(ov);
+        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = to_f16x4(ov);
       }
     }
   }
 }
 
-template <int HD, int NCH, int NW, bool HWX>
-void launch_attn_x(pfhip_backend* b, const AttnArgs& a) {
-  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;
-  const size_t lds = (size_t)(ROWS * (HD + 8) + HD * (ROWS + 8)) * sizeof(_Float16);
-  static bool attr_set = false;
+
+// The reference's GPU-path numerics (fp16): the softmax exponentials use the
+// hardware exp2 (v_exp_f32, about 1 ulp) on scores in units of log2(e), as
+// the GPU shader uses the WGSL exp (native/shaders/banded_attention.wgsl:
+// 100-113), and the output is stored with the hardware fp16 conversion.
+// After the max pass, one pass per 32-key chunk computes e = 2^(s - m), adds
+// it to the row sum and feeds it (as fp16 hi + lo) straight into P.V, so the
+// exponentials of one chunk overlap the MFMAs of the previous one; the
+// normalisation by the row sum is applied to the f32 output accumulators
+// (sum_i (e_i / l) v_i = (sum_i e_i v_i) / l up to f32 rounding). Requires
+// scale > 0 (the row maximum is taken over the unscaled scores).
+template <int HD, int NCH, int NW>
+__global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
+  constexpr int QB = 16 * NW;                // query tokens per workgroup
+  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
+  constexpr int LDK = HD + 8;                // K row stride (halves)
+  constexpr int LDV = ROWS + 8;              // V^T row stride (halves)
+  constexpr int NDH = HD / 32;               // MFMA K-steps over head_dim for Q.K
+  constexpr int NDT = HD / 16;               // 16-row dim tiles of O^T
+  extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+  _Float16* Ks = smem;                       // [ROWS][LDK]
+  _Float16* Vt = smem + ROWS * LDK;          // [HD][LDV]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int t0 = blockIdx.x * QB;
+  const int g = blockIdx.y;                  // kv head
+  const int bseq = blockIdx.z;
+  const int T = a.T, W = a.window;
+  const size_t seq0 = (size_t)bseq * T;
+  const int kbase = t0 - W;                  // key index of staged row 0
+
+  stage_kv<HD, ROWS, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
+  __syncthreads();
+
+  const int tq0 = t0 + 16 * wave;            // this wave's first query
+  const int tq = tq0 + l16;                  // this lane's query
+  const int rb = 16 * wave;                  // staged row of key tq0 - W
+  const int kw = tq0 - W;                    // key at chunk offset 0 of this wave
+  const bool q_ok = tq < T;
+  const int ws = max(0, tq - W), we = min(T, tq + W + 1);
+  const int lo0 = ws - kw, hi0 = we - kw;    // the window [lo, hi) as chunk offsets
+  // wave-uniform: chunks wholly inside every lane's window (lanes past T do not constrain them)
+  const int full_lo = wave_max_i(q_ok ? lo0 : 0);
+  const int full_hi = wave_min_i(q_ok ? hi0 : 1 << 20);
+  const bool masked = a.mask != nullptr;
+  const int G = a.Hq / a.Hkv;
+  constexpr float LOG2_E = 1.44269504088896340736f;
+  const float sscale = a.scale * LOG2_E;     // scores in the exponent's units
+
+  for (int hh = 0; hh < G; ++hh) {
+    const int hq = g * G + hh;
+    // opaque per-head copies of the window bounds (see k_banded_attention)
+    int lo = lo0, hi = hi0;
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    h8_t qf[NDH];
+#pragma unroll
+    for (int dh = 0; dh < NDH; ++dh) {
+      u4_t v = {0u, 0u, 0u, 0u};
+      if (q_ok) v = *reinterpret_cast<const u4_t*>(a.q + (seq0 + tq) * a.q_stride + hq * HD + 32 * dh + 8 * lg);
+      qf[dh] = __builtin_bit_cast(h8_t, v);
+    }
+    const float sink = a.sinks ? a.sinks[hq] * LOG2_E : -INFINITY;
+
+    // ---- pass 1: unscaled scores for the whole band, kept in registers;
+    // slots outside the query's window and masked keys hold -inf. The K
+    // fragments of chunk c + 1 are read while chunk c is processed.
+    float s[NCH][2][4];
+    float mr = -INFINITY;
+    h8_t kf[2][NDH], kn[2][NDH];
+    auto load_k = [&](int c, h8_t (&dst)[2][NDH]) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int dh = 0; dh < NDH; ++dh)
+          dst[kt][dh] = *reinterpret_cast<const h8_t*>(&Ks[(rb + 32 * c + 16 * kt + l16) * LDK + 32 * dh + 8 * lg]);
+    };
+    load_k(0, kf);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c + 1 < NCH) load_k(c + 1, kn);
+      f4_t acc[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][0], qf[0], f4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int dh = 1; dh < NDH; ++dh)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][dh], qf[dh], acc[kt]);
+      if (!masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[c][kt][r] = acc[kt][r];
+          mr = fmaxf(mr, fmaxf(fmaxf(acc[kt][0], acc[kt][1]), fmaxf(acc[kt][2], acc[kt][3])));
+        }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = 32 * c + 16 * kt + 4 * lg + r;
+            bool valid = (off >= lo) & (off < hi);
+            if (masked) valid = valid && a.mask[seq0 + kw + off] != 0;
+            const float sv = valid ? acc[kt][r] : -INFINITY;
+            s[c][kt][r] = sv;
+            mr = fmaxf(mr, sv);
+          }
+      }
+      if (c + 1 < NCH) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int dh = 0; dh < NDH; ++dh) kf[kt][dh] = kn[kt][dh];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // lanes l, l^16, l^32, l^48 hold the same query
+    mr = fmaxf(mr, __shfl_xor(mr, 16, 64));
+    mr = fmaxf(mr, __shfl_xor(mr, 32, 64));
+    // max over the scaled scores (scaling by sscale > 0 keeps the order) and the sink;
+    // -inf only without a sink and with no valid key (every e is then 0)
+    float m = fmaxf(mr * sscale, sink);
+    m = m == -INFINITY ? 0.0f : m;
+    const float nm = -m;
+
+    // ---- pass 2: e = 2^(s sscale - m), the row sum, and O^T += V^T . E^T.
+    // e enters the MFMA as fp16 hi + lo: hi is e cut to 11 significant bits
+    // (exact in fp16 for e >= 2^-14), lo = e - hi (exact in f32) rounded to
+    // fp16, so hi + lo carries ~22 bits of e (below 2^-14, an absolute error
+    // under 2^-24 against the row maximum's 1). The V^T fragments of chunk
+    // c + 1 are read while chunk c is processed.
+    float l = 0.0f;
+    f4_t o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    h8_t vf[NDT], vn[NDT];
+    auto load_v = [&](int c, h8_t (&dst)[NDT]) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const _Float16* vr = &Vt[(16 * dt + l16) * LDV + rb + 32 * c + 4 * lg];
+        const h4_t v0 = *reinterpret_cast<const h4_t*>(vr);
+        const h4_t v1 = *reinterpret_cast<const h4_t*>(vr + 16);
+        dst[dt] = h8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      }
+    };
+    load_v(0, vf);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c + 1 < NCH) load_v(c + 1, vn);
+      h8_t ph, pl;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
+          l += e0;
+          l += e1;
+          const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
+          const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
+          const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+          const h2_t hl = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
+          ph[4 * kt + r] = hh[0];
+          ph[4 * kt + r + 1] = hh[1];
+          pl[4 * kt + r] = hl[0];
+          pl[4 * kt + r + 1] = hl[1];
+        }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
+      if (c + 1 < NCH) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) vf[dt] = vn[dt];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    l += __builtin_amdgcn_exp2f(sink - m);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // lane holds out[tq][hq*HD + 16 dt + 4 lg + r]
+    if (q_ok) {
+      uint16_t* orow = a.out + (seq0 + tq) * a.out_stride + hq * HD;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const float ov[4] = {o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv};
+        *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = to_f16x4_native(ov);
+      }
+    }
+  }
+}
+
+template <typename Kern>
+void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, int rows, int qb, int nt, bool& attr_set) {
+  const size_t lds = (size_t)(rows * (a.head_dim + 8) + a.head_dim * (rows + 8)) * sizeof(_Float16);
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_banded_attention<HD, NCH, NW, HWX>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)lds));
     attr_set = true;
   }
-  dim3 grid((a.T + 16 * NW - 1) / (16 * NW), a.Hkv, a.B);
+  dim3 grid((a.T + qb - 1) / qb, a.Hkv, a.B);
   ProfScope ps(b, "banded_attention");
-  hipLaunchKernelGGL((k_banded_attention<HD, NCH, NW, HWX>), grid, dim3(64 * NW), lds, b->stream, a);
+  hipLaunchKernelGGL(kern, grid, dim3(nt), lds, b->stream, a);
   PF_HIP(hipGetLastError());
 }
 
 template <int HD, int NCH, int NW>
 void launch_attn(pfhip_backend* b, const AttnArgs& a) {
-  if (a.hw_exp) launch_attn_x<HD, NCH, NW, true>(b, a);
-  else launch_attn_x<HD, NCH, NW, false>(b, a);
+  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;
+  if (a.hw_exp) {
+    static bool attr_set = false;
+    launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW>, ROWS, 16 * NW, 64 * NW, attr_set);
+  } else {
+    static bool attr_set = false;
+    launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, ROWS, 16 * NW, 64 * NW, attr_set);
+  }
 }
 
 template <int HD>
@@ -303,6 +506,7 @@ void banded_attention(pfhip_backend* b, const AttnArgs& a) {
   // 16 + 2W keys per 16-query tile must fit nine 32-key chunks (LDS: 110 KB)
   PF_CHECK(a.window >= 0 && a.window <= 128, "banded_attention: window must be in [0, 128]");
   PF_CHECK(a.q && a.k && a.v && a.out, "banded_attention: null operand");
+  PF_CHECK(!a.hw_exp || a.scale > 0.0f, "banded_attention: the hardware-exp softmax needs scale > 0");
   PF_CHECK(a.q_stride % 8 == 0 && a.k_stride % 8 == 0 && a.v_stride % 8 == 0 && a.out_stride % 4 == 0,
            "banded_attention: row strides must allow 16-byte loads");
   PF_CHECK(((uintptr_t)a.q & 15) == 0 && ((uintptr_t)a.k & 15) == 0 && ((uintptr_t)a.v & 15) == 0 &&
