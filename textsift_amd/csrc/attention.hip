@@ -47,14 +47,28 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
-// Stages the workgroup's keys kbase .. kbase + ROWS - 1 of kv head g: K
-// row-major [ROWS][HD + 8], V transposed [HD][ROWS + 8]; rows outside
-// [0, T) are zero (their scores are masked).
-template <int HD, int ROWS, int NT>
+// LDS geometry of a workgroup of NW waves x 16 queries with NCH 32-key
+// chunks per wave: ROWS staged keys (every wave's chunks, rounded up to 32),
+// K row-major [ROWS][LDK], V transposed [HD][LDV]. LDK = HD + 8 halves
+// (36 dwords for HD = 64: the 16-byte K-fragment reads of 8 consecutive rows
+// hit distinct banks); LDV = ROWS + 4 halves (2 mod 4 dwords: the 8-byte
+// V^T-fragment reads of 16 consecutive rows hit distinct banks).
+template <int HD, int NCH, int NW>
+struct AttnGeom {
+  static constexpr int ROWS = (16 * (NW - 1) + 32 * NCH + 31) / 32 * 32;
+  static constexpr int LDK = HD + 8;
+  static constexpr int LDV = ROWS + 4;
+  static constexpr size_t LDS = (size_t)(ROWS * LDK + HD * LDV) * 2;
+  static_assert(LDV % 8 == 4, "V^T row stride must be 2 mod 4 dwords");
+};
+
+// Stages the workgroup's keys kbase .. kbase + ROWS - 1 of kv head g into
+// Ks / Vt (layout of AttnGeom); rows outside [0, T) are zero (their scores
+// are masked).
+template <int HD, int ROWS, int LDK, int LDV, int NT>
 __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float16* Vt, size_t seq0, int g, int kbase,
                                          int tid) {
-  constexpr int LDK = HD + 8, LDV = ROWS + 8;
-  static_assert(ROWS % 4 == 0, "V^T staging writes 4 keys at a time");
+  static_assert(ROWS % 32 == 0, "V^T staging: whole groups of 8 x 4 keys");
   const int T = a.T;
   for (int i = tid; i < ROWS * (HD / 8); i += NT) {
     const int r = i / (HD / 8), c = i % (HD / 8);
@@ -63,8 +77,10 @@ __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float
     if (key >= 0 && key < T) kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
     *reinterpret_cast<u4_t*>(&Ks[r * LDK + c * 8]) = kv;
   }
-  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += NT) {  // 4 keys x 8 dims per thread
-    const int r4 = (i / (HD / 8)) * 4, c = i % (HD / 8);
+  // 4 keys x 8 dims per thread; 8 consecutive lanes take 32 consecutive keys
+  // of the same 8 dims, so each V^T row write of 16 lanes covers distinct banks
+  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += NT) {
+    const int c = (i >> 3) % (HD / 8), r4 = ((i & 7) + 8 * ((i >> 3) / (HD / 8))) * 4;
     h8_t vh[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -85,13 +101,11 @@ __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float
 // tile.
 template <int HD, int NCH, int NW>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
+  using GE = AttnGeom<HD, NCH, NW>;
   constexpr int QB = 16 * NW;                // query tokens per workgroup
-  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
-  constexpr int LDK = HD + 8;                // K row stride (halves)
-  constexpr int LDV = ROWS + 8;              // V^T row stride (halves)
+  constexpr int ROWS = GE::ROWS, LDK = GE::LDK, LDV = GE::LDV;
   constexpr int NDH = HD / 32;               // MFMA K-steps over head_dim for Q.K
   constexpr int NDT = HD / 16;               // 16-row dim tiles of O^T
-  static_assert(ROWS % 4 == 0, "V^T staging writes 4 keys at a time");
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   _Float16* Ks = smem;                       // [ROWS][LDK]
   _Float16* Vt = smem + ROWS * LDK;          // [HD][LDV]
@@ -105,7 +119,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const size_t seq0 = (size_t)bseq * T;
   const int kbase = t0 - W;                  // key index of staged row 0
 
-  stage_kv<HD, ROWS, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
+  stage_kv<HD, ROWS, LDK, LDV, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
   __syncthreads();
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
@@ -282,10 +296,9 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 // scale > 0 (the row maximum is taken over the unscaled scores).
 template <int HD, int NCH, int NW>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
+  using GE = AttnGeom<HD, NCH, NW>;
   constexpr int QB = 16 * NW;                // query tokens per workgroup
-  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;  // staged key rows (every wave's chunks)
-  constexpr int LDK = HD + 8;                // K row stride (halves)
-  constexpr int LDV = ROWS + 8;              // V^T row stride (halves)
+  constexpr int ROWS = GE::ROWS, LDK = GE::LDK, LDV = GE::LDV;
   constexpr int NDH = HD / 32;               // MFMA K-steps over head_dim for Q.K
   constexpr int NDT = HD / 16;               // 16-row dim tiles of O^T
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
@@ -301,7 +314,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   const size_t seq0 = (size_t)bseq * T;
   const int kbase = t0 - W;                  // key index of staged row 0
 
-  stage_kv<HD, ROWS, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
+  stage_kv<HD, ROWS, LDK, LDV, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
   __syncthreads();
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
@@ -400,7 +413,10 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     // fp16, so hi + lo carries ~22 bits of e (below 2^-14, an absolute error
     // under 2^-24 against the row maximum's 1). The V^T fragments of chunk
     // c + 1 are read while chunk c is processed.
-    float l = 0.0f;
+    // The row sum runs on the matrix cores too: an all-ones A operand gives
+    // every output row sum_k (hi + lo)_k for the lane's query.
+    const h8_t ones = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+    f4_t lsum = f4_t{0.f, 0.f, 0.f, 0.f};
     f4_t o[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -425,8 +441,6 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         for (int r = 0; r < 4; r += 2) {
           const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
           const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
-          l += e0;
-          l += e1;
           const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
           const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
           const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
@@ -438,17 +452,17 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
+      lsum = mfma16x16x32(ones, ph, lsum);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
+      lsum = mfma16x16x32(ones, pl, lsum);
       if (c + 1 < NCH) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) vf[dt] = vn[dt];
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    l += __builtin_amdgcn_exp2f(sink - m);
+    const float l = lsum[0] + __builtin_amdgcn_exp2f(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     // lane holds out[tq][hq*HD + 16 dt + 4 lg + r]
     if (q_ok) {
@@ -463,8 +477,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
 }
 
 template <typename Kern>
-void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, int rows, int qb, int nt, bool& attr_set) {
-  const size_t lds = (size_t)(rows * (a.head_dim + 8) + a.head_dim * (rows + 8)) * sizeof(_Float16);
+void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, size_t lds, int qb, int nt, bool& attr_set) {
   if (!attr_set) {
     PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)lds));
@@ -478,13 +491,14 @@ void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, int rows, in
 
 template <int HD, int NCH, int NW>
 void launch_attn(pfhip_backend* b, const AttnArgs& a) {
-  constexpr int ROWS = 16 * (NW - 1) + 32 * NCH;
+  constexpr size_t LDS = AttnGeom<HD, NCH, NW>::LDS;
+  static_assert(LDS <= 160 * 1024, "attention tile exceeds the LDS");
   if (a.hw_exp) {
     static bool attr_set = false;
-    launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW>, ROWS, 16 * NW, 64 * NW, attr_set);
+    launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW>, LDS, 16 * NW, 64 * NW, attr_set);
   } else {
     static bool attr_set = false;
-    launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, ROWS, 16 * NW, 64 * NW, attr_set);
+    launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, LDS, 16 * NW, 64 * NW, attr_set);
   }
 }
 
