@@ -44,8 +44,8 @@ KERNEL_LABELS = [
     ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true>")),
     ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true>")),
     ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false>")),
-    ("gemm_o", ("k_gemm_w4<5, 64", "(pf::Epi)0, false>")),
-    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)1, false>")),
+    ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false>")),
+    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)5, false>")),
     ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false>")),
     ("banded_attention", ("k_banded_attention",)),
     ("moe_combine_norm", ("k_moe_combine",)),

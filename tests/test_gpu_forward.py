@@ -251,3 +251,39 @@ def test_stream_batcher_on_gpu(small):
         print(f"stream {s}: {len(ref)} spans, identical {got[s] == ref}")
         if exact:
             assert got[s] == ref
+
+
+@pytest.mark.parametrize("kind", ["random", "ties", "nan"])
+def test_fused_router_topk_bit_exact(kind):
+    """The router GEMM's top-4 epilogue (fp16 numerics, 128 experts) against
+    the oracle's insertion top-k (zig/wasm_exports.zig:367-426) on the logits
+    the same GEMM wrote: identical expert ids and weights. "ties" zeroes the
+    router weights (every nibble equals its zero-point), so each logit is its
+    fp16 bias, rounded to integers: many exact ties, within and across the
+    two halves of the row the epilogue merges. "nan" adds two NaN biases
+    (the sequential insertion path)."""
+    E, T, Vv = 128, 300, 512
+    w = synth.make_model_weights(PF_CONFIG, seed=77, num_layers=1, num_experts=E, vocab_size=Vv)
+    if kind != "random":
+        w["layers.0.router.int4"][:] = 0x88
+        w["layers.0.router.zp"][:] = 0x88
+        bias = np.round(synth.normal(78, E, 0.0, 1.5)).astype(np.float16)
+        if kind == "nan":
+            bias[[5, 70]] = np.nan
+        w["layers.0.router.bias"] = bias.view(np.uint16)
+    be = HipBackend(w, precision=_native.PRECISION_FP16)
+    be.warmup()
+    m = be.model
+    m.enable_taps(True)
+    be.forward(synth.token_ids(79, T, Vv), np.ones(T, np.uint8))
+    rl = m.tap("router.0", np.float32, T * E).reshape(T, E)
+    idx = m.tap("ridx.0", np.int32, T * 4).reshape(T, 4)
+    rw = m.tap("rw.0", np.float32, T * 4).reshape(T, 4)
+    m.enable_taps(False)
+    be.dispose()
+    idx_ref, val_ref = oracle.topk(rl, T, E, 4)
+    w_ref = oracle.softmax(val_ref, T, 4)
+    if kind == "ties":
+        assert len(np.unique(rl[0])) < 16  # the rows really are tie-heavy
+    assert np.array_equal(idx, idx_ref)
+    assert np.allclose(rw, w_ref, rtol=0.0, atol=2e-7, equal_nan=True)

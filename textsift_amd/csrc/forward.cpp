@@ -374,14 +374,20 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
       a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
       a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
+      // fp16 numerics with the model's 128 experts and top-4: the router
+      // GEMM's epilogue selects the experts (bit-identical to router_topk)
+      const bool fused_topk = f16 && E == 128 && K == 4;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.router4.w); a.wsz = L.router4.sz;
-        gemm_w4(b, a, XKind::F16, Epi::F32, false, 128, 2, "gemm_router");
+        if (fused_topk) {
+          a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
+        }
+        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, 128, 2, "gemm_router");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
       }
+      if (!fused_topk) router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
     }
-    router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
     record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
     record_tap(m, "ridx." + tag, s.ridx, (size_t)M * K * 4);
     record_tap(m, "rw." + tag, s.rw, (size_t)M * K * 4);

@@ -278,7 +278,9 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
     case Epi::ROPE_F16: return launch<BT, SPLIT, Epi::ROPE_F16, GROUPED>(b, a, name);
     case Epi::SWIGLU_SPLIT: return launch<BT, SPLIT, Epi::SWIGLU_SPLIT, GROUPED>(b, a, name);
     case Epi::SWIGLU_F16: return launch<BT, SPLIT, Epi::SWIGLU_F16, GROUPED>(b, a, name);
+    case Epi::F32_TOPK: break;
   }
+  throw Error("gemm_int4: unsupported epilogue");
 }
 
 }  // namespace

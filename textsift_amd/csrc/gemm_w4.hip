@@ -36,6 +36,7 @@
 #include "common.cuh"
 #include "epilogue.cuh"
 #include "pfhip_internal.h"
+#include "topk.cuh"
 
 namespace pf {
 
@@ -94,8 +95,9 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // units, units XOR-swizzled by row & SWM for conflict-free LDS writes).
 template <int WF, int BT, Epi EPI>
 struct StagedOut {
-  static constexpr bool OK = EPI == Epi::F32 || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16;
-  static constexpr int ESZ = EPI == Epi::F32 ? 4 : 2;
+  static constexpr bool F32OUT = EPI == Epi::F32 || EPI == Epi::F32_TOPK;
+  static constexpr bool OK = F32OUT || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16;
+  static constexpr int ESZ = F32OUT ? 4 : 2;
   static constexpr int CF = EPI == Epi::SWIGLU_F16 ? 8 : 16;
   static constexpr int FB = CF * ESZ;
   static constexpr int PS = FB / 4;
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
     // which costs the gate_up GEMM about a fifth of its time).
     char* ob = reinterpret_cast<char*>(xs_lds);
     u2_t ow[WF][TJ];  // packed fp16 results (F32 writes the accumulators)
-    if constexpr (EPI != Epi::F32) {
+    if constexpr (!SO::F32OUT) {
 #pragma unroll
       for (int f = 0; f < WF; ++f) {
         const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
           const int row = 16 * tj + l16;
           const int byte = (wave * SO::FG + fl) * SO::FB + lg * SO::PS;
           char* dst = ob + row * SO::PRB + (((byte >> 4) ^ (row & SO::SWM)) << 4) + (byte & 15);
-          if constexpr (EPI == Epi::F32) *reinterpret_cast<f4_t*>(dst) = acc[f][tj];
+          if constexpr (SO::F32OUT) *reinterpret_cast<f4_t*>(dst) = acc[f][tj];
           else if constexpr (EPI == Epi::SWIGLU_F16) *reinterpret_cast<uint32_t*>(dst) = ow[f][tj].x;
           else *reinterpret_cast<u2_t*>(dst) = ow[f][tj];
         }
@@ -367,8 +369,75 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
               *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
       }
     }
+    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 == 256) {
+      // Router top-4 of every row from the staged tile (all N == 128 logits
+      // of BT rows are in LDS): two threads per row each take the top-4 of
+      // one half by the reference's insertion rule, then the halves merge by
+      // (value descending, index ascending), which is what the insertion
+      // over the whole row yields without NaNs; a row with a NaN replays the
+      // sequential insertion over all 128 logits.
+      const int row = tid >> 1, half = tid & 1;
+      const char* rb = ob + row * SO::PRB;
+      auto at = [&](int c) -> float {
+        return *reinterpret_cast<const float*>(rb + (((c >> 2) ^ (row & SO::SWM)) << 4) + (c & 3) * 4);
+      };
+      float V[4];
+      int I[4];
+      topk_insertion<4>([&](int c) { return at(64 * half + c); }, 64, V, I);
+      bool nan = false;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const f4_t q = *reinterpret_cast<const f4_t*>(rb + (((16 * half + u) ^ (row & SO::SWM)) << 4));
+        nan = nan | (q[0] != q[0]) | (q[1] != q[1]) | (q[2] != q[2]) | (q[3] != q[3]);
+      }
+      nan = nan | (__shfl_xor((int)nan, 1, 64) != 0);
+      float BV[4];
+      int BI[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        BV[k] = __shfl_xor(V[k], 1, 64);
+        BI[k] = __shfl_xor(I[k], 1, 64) + 64;
+      }
+      if (half == 0 && row < rows) {
+        float RV[4];
+        int RI[4];
+        if (nan) {
+          topk_insertion<4>(at, 128, RV, RI);
+        } else {
+          // rank of each candidate among the 8; the first half (lower ids) wins ties
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            RV[k] = 0.0f;
+            RI[k] = 0;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            int ra = i, rbk = i;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              ra += BV[j] > V[i];
+              rbk += V[j] >= BV[i];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              if (ra == k) {
+                RV[k] = V[i];
+                RI[k] = I[i];
+              }
+              if (rbk == k) {
+                RV[k] = BV[i];
+                RI[k] = BI[i];
+              }
+            }
+          }
+        }
+        const size_t t = (size_t)(row0 + row);
+        topk_write<4>(RV, RI, p.topk_wscale, p.topk_idx + t * 4, p.topk_w + t * 4);
+      }
+    }
     return;
   }
+
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
     const int n = ncol[f];
@@ -433,6 +502,9 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
     case Epi::ROPE_F16: return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED>(b, a, name);
     case Epi::SWIGLU_SPLIT: break;
     case Epi::SWIGLU_F16: return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED>(b, a, name);
+    case Epi::F32_TOPK:
+      if constexpr (WF == 2 && BT == 128 && !GROUPED) return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED>(b, a, name);
+      break;
   }
   throw Error("gemm_w4: unsupported epilogue");
 }
@@ -504,13 +576,18 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   // partial 16-byte unit at column N
   GemmArgs g = a;
   {
-    const int esz = epi == Epi::F32 ? 4 : 2;
+    const int esz = epi == Epi::F32 || epi == Epi::F32_TOPK ? 4 : 2;
     const int ocols = epi == Epi::SWIGLU_F16 ? a.N / 2 : a.N;
-    g.out_staged = (epi == Epi::F32 || epi == Epi::F16 || epi == Epi::ROPE_F16 || epi == Epi::SWIGLU_F16) &&
+    g.out_staged = (epi == Epi::F32 || epi == Epi::F32_TOPK || epi == Epi::F16 || epi == Epi::ROPE_F16 ||
+                    epi == Epi::SWIGLU_F16) &&
                    ocols % (16 / esz) == 0 && (a.ldo * esz) % 16 == 0 &&
                    (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && (epi != Epi::SWIGLU_F16 || a.N % 16 == 0);
   }
   PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
+  if (epi == Epi::F32_TOPK)
+    PF_CHECK(!grouped && tile_t == 128 && wf == 2 && a.N == 128 && a.topk_k == 4 && a.topk_idx && a.topk_w &&
+                 g.out_staged,
+             "gemm_w4: the top-k epilogue needs N == 128, K == 4, the 128 x 128 tile and 16-byte aligned f32 rows");
   if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);

@@ -6,6 +6,7 @@
 #include "common.cuh"
 #include "epilogue.cuh"
 #include "pfhip_internal.h"
+#include "topk.cuh"
 
 namespace pf {
 
@@ -221,33 +222,10 @@ __global__ void k_rope(uint16_t* qk, const uint16_t* cs, const uint16_t* sn, int
 }
 
 // ----------------------------------------------------------------------------
-// Router top-k + softmax (topk_partial_f32 :367-426, softmax_f32 :919-958).
-// One thread per token replays the reference's insertion order exactly:
-// output sorted by logit descending, ties keep the lower expert id first.
+// Router top-k + softmax (topk_partial_f32 :367-426, softmax_f32 :919-958;
+// the insertion order and the weights are in topk.cuh): output sorted by
+// logit descending, ties keep the lower expert id first.
 constexpr int MAXK = 8;
-// The reference's insertion top-k (sorted descending; an equal value never
-// displaces an earlier index) on one row, sequentially.
-template <int K>
-__device__ void topk_insertion(const float* x, int E, float* V, int* I) {
-  for (int i = 0; i < K; ++i) { I[i] = i; V[i] = x[i]; }
-  for (int s = 1; s < K; ++s)
-    for (int j = s; j > 0 && V[j] > V[j - 1]; --j) {
-      float tv = V[j]; V[j] = V[j - 1]; V[j - 1] = tv;
-      int ti = I[j]; I[j] = I[j - 1]; I[j - 1] = ti;
-    }
-  for (int c = K; c < E; ++c) {
-    const float v = x[c];
-    if (v > V[K - 1]) {
-      V[K - 1] = v;
-      I[K - 1] = c;
-      for (int j = K - 1; j > 0 && V[j] > V[j - 1]; --j) {
-        float tv = V[j]; V[j] = V[j - 1]; V[j - 1] = tv;
-        int ti = I[j]; I[j] = I[j - 1]; I[j - 1] = ti;
-      }
-    }
-  }
-}
-
 // One wave per token; lane l holds logits l, l+64, l+128, l+192. Without
 // NaNs the insertion top-k equals K rounds of "largest value, lowest index
 // among equal values", done as wave reductions; a row with a NaN takes the
@@ -273,7 +251,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
   float V[K];
   int I[K];
   if (__any(nan)) {
-    if (lane == 0) topk_insertion<K>(x, E, V, I);
+    if (lane == 0) topk_insertion<K>([&](int c) { return x[c]; }, E, V, I);
     // broadcast lane 0's result
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -306,20 +284,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
       for (int j = 0; j < TOPK_PL; ++j) live[j] = live[j] & (lane + 64 * j != bi);
     }
   }
-  if (lane == 0) {
-    float mx = V[0];
-#pragma unroll
-    for (int c = 1; c < K; ++c) if (V[c] > mx) mx = V[c];
-    float e[K], sum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < K; ++c) { e[c] = expf(V[c] - mx); sum += e[c]; }
-    const float inv = sum > 0.0f ? 1.0f / sum : 1.0f / (float)K;
-#pragma unroll
-    for (int c = 0; c < K; ++c) {
-      idx[(size_t)t * K + c] = I[c];
-      w[(size_t)t * K + c] = (e[c] * inv) * wscale;
-    }
-  }
+  if (lane == 0) topk_write<K>(V, I, wscale, idx + (size_t)t * K, w + (size_t)t * K);
 }
 
 // ----------------------------------------------------------------------------

@@ -87,7 +87,9 @@ void set_err(char* err, size_t cap, const std::string& msg);
 // fp16 planes, hi = fp16(v) and lo = fp16(v - hi) (22 significant bits), which
 // enter the MFMA as two products per block into the same partial sum.
 enum class XKind { F16, SPLIT };
-enum class Epi { F16, F32, ROPE_F16, SWIGLU_SPLIT, SWIGLU_F16 };
+// F32_TOPK (gemm_w4, N == 128, one column tile): F32, then the router
+// top-4 + softmax of each output row into topk_idx / topk_w.
+enum class Epi { F16, F32, ROPE_F16, SWIGLU_SPLIT, SWIGLU_F16, F32_TOPK };
 
 struct GemmArgs {
   const void* x = nullptr;       // activations [rows][K] fp16 (the hi plane in SPLIT mode)
@@ -116,6 +118,11 @@ struct GemmArgs {
   const uint16_t* rope_pairs = nullptr;  // [seq_len][head_dim/2][cos, sin] fp16 bits (gemm_w4)
   int seq_len = 0;
   int rope_cols = 0;                   // columns [0, rope_cols) are rotated
+  // F32_TOPK epilogue: [M][topk_k] expert ids and routing weights (times topk_wscale)
+  int32_t* topk_idx = nullptr;
+  float* topk_w = nullptr;
+  int topk_k = 0;
+  float topk_wscale = 1.0f;
   // gemm_w4: stage the output tile through LDS and store whole 16-byte units
   // (set by gemm_w4 itself when the output layout allows it)
   int out_staged = 0;
