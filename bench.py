@@ -44,6 +44,7 @@ KERNEL_LABELS = [
     ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true>")),
     ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true>")),
     ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false>")),
+    ("gemm_o_add_rmsnorm", ("k_gemm_w4_rownorm",)),
     ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false>")),
     ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)5, false>")),
     ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false>")),
@@ -147,6 +148,7 @@ def gemm_flops(cfg, M):
     return {
         "gemm_qkv_rope": 2.0 * M * (hq + 2 * hk) * hd * D,
         "gemm_o": 2.0 * M * D * hq * hd,
+        "gemm_o_add_rmsnorm": 2.0 * M * D * hq * hd,  # the O GEMM with the residual add + norm fused
         "gemm_router": 2.0 * M * E * D,
         "gemm_moe_gate_up": 2.0 * S * 2 * F * D,
         "gemm_moe_down": 2.0 * S * D * F,

@@ -361,13 +361,17 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.out = s.o; a.ldo = D; a.M = M; a.N = D; a.K = Hq * hd;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.o4.w); a.wsz = L.o4.sz;
-        gemm_w4(b, a, XKind::F16, Epi::F16, false, 128, 4, "gemm_o");
+        if (D == 640 && (Hq * hd == 640 || Hq * hd == 896)) {  // whole rows per workgroup: add + norm fused
+          gemm_w4_add_rmsnorm(b, a, h, L.ln_post, s.h2, s.xn_hi, c.eps);
+        } else {
+          gemm_w4(b, a, XKind::F16, Epi::F16, false, 128, 4, "gemm_o");
+          add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
+        }
       } else {
         gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
+        add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
       }
     }
-    if (f16) add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
-    else add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
     record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
     {
       GemmArgs a;

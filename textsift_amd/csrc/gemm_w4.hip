@@ -595,6 +595,265 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   throw Error("gemm_w4: unsupported (tile_t, wf) = (" + std::to_string(tile_t) + ", " + std::to_string(wf) + ")");
 }
 
+// ---------------------------------------------------------------- O GEMM + residual + RMSNorm
+//
+// The attention output projection with the block's post-attention residual
+// add and RMSNorm fused into the epilogue (the O MatMulNBits, add_fp16 and
+// add_rmsnorm_fp16_to_f32 of zig/wasm_exports.zig:560-707, 969-990,
+// 288-350, in the GPU shaders' fp16 numerics):
+//   o   = fp16(x . w16^T + bias)                      (the GEMM output)
+//   h2  = fp16(o + h)                                 (the new residual)
+//   xn  = fp16(h2 / sqrt(mean((o + h)^2) + eps) * g)  (sum of squares of the
+//         unrounded f32 sum, normalising the rounded one)
+// A workgroup of 8 waves owns 64 whole rows (all N = 8 x 5 x 16 = 640
+// columns), so the row's sum of squares is reduced in the workgroup (lanes,
+// then waves through LDS) and o never goes to memory.
+namespace {
+
+constexpr int RN_NW = 8, RN_WF = 5, RN_BT = 64;
+constexpr int RN_BN = RN_NW * RN_WF * 16;  // 640
+
+// copy16_to_lds issued as inline assembly: the compiler then does not know
+// that it writes LDS and does not make every workgroup barrier wait for all
+// such copies in flight (vmcnt(0)); the kernel waits for the ones it needs
+// itself. Clobbers M0, which nothing else in the kernel uses.
+__device__ __forceinline__ void copy16_to_lds_async(const void* src, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_byte) : "memory", "m0");
+}
+
+// C = K / 128 chunks, fully unrolled: chunk c + 2 is loaded while chunk c
+// is computed (three activation buffers, three weight register sets), so a
+// load has two chunks of MFMAs to land; with one 8-wave workgroup per CU
+// nothing else hides it.
+template <int C>
+__global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, const uint16_t* __restrict__ resid,
+                                                                   const uint16_t* __restrict__ gamma,
+                                                                   uint16_t* __restrict__ h_out,
+                                                                   uint16_t* __restrict__ xn_out, float eps) {
+  constexpr int NW8 = RN_NW, WF = RN_WF, BT = RN_BT, TJ = BT / 16;
+  constexpr int XI = BT * KC * 2 / 1024 / NW8;  // 1 KB direct loads per wave per chunk
+  constexpr int PLANE = BT * KC;                // halves per buffer
+  static_assert(XI >= 1 && BT * KC * 2 % (1024 * NW8) == 0, "whole 1 KB copies per wave");
+  // vector memory instructions per lane and chunk, issued in this order:
+  // WF weight and WF scale loads, then XI activation copies
+  constexpr int VM_PER_CHUNK = 2 * WF + XI;
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [3][BT][KC] swizzled, then the row sums
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int tt = xcd_remap(blockIdx.x, gridDim.x);
+  const int row0 = tt * BT;
+  const int rows = min(BT, p.M - row0);
+  if (rows <= 0) return;
+  const int kd = p.K >> 3, nb = p.K >> 5;
+
+  const uint32_t* __restrict__ W = reinterpret_cast<const uint32_t*>(p.w);
+  const uint32_t* wptr[WF];
+  const uint32_t* sptr[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) {
+    const int n = (wave * WF + f) * 16 + l16;
+    wptr[f] = W + (size_t)n * kd + lg * 4;
+    sptr[f] = p.wsz + (size_t)n * nb + lg;
+  }
+  const uint16_t* __restrict__ xsrc = static_cast<const uint16_t*>(p.x);
+  int xoff[XI];
+#pragma unroll
+  for (int m = 0; m < XI; ++m) {
+    const int r = (m * NW8 + wave) * 4 + lg;
+    xoff[m] = (row0 + min(r, rows - 1)) * p.ldx + ((l16 ^ (r & 15)) << 3);
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)xs_lds;
+  auto load_x = [&](int c, int buf) {
+#pragma unroll
+    for (int m = 0; m < XI; ++m)
+      copy16_to_lds_async(xsrc + xoff[m] + c * KC,
+                          __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(buf * PLANE + (m * NW8 + wave) * 512) * 2));
+  };
+  u4_t wraw[C][WF];  // only three chunks' sets are live at a time
+  uint32_t sz[C][WF];
+  auto load_w = [&](int c) {
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      wraw[c][f] = *reinterpret_cast<const u4_t*>(wptr[f] + c * 16);
+      sz[c][f] = sptr[f][c * 4];
+    }
+  };
+
+  int ncol[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) ncol[f] = (wave * WF + f) * 16 + 4 * lg;
+  f4_t acc[WF][TJ];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) {
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+      const h4_t bh = __builtin_bit_cast(h4_t, *reinterpret_cast<const u2_t*>(p.bias + ncol[f]));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[r] = (float)bh[r];
+    }
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
+  }
+
+  auto compute = [&](int c) {
+    h2_t off[WF], sc[WF];
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      const h2_t pr = __builtin_bit_cast(h2_t, sz[c][f]);
+      off[f] = h2_t{pr.x, pr.x};
+      sc[f] = h2_t{pr.y, pr.y};
+    }
+    const _Float16* xb = xs_lds + (c % 3) * PLANE;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h8_t wd[WF];
+#pragma unroll
+      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wraw[c][f][j], off[f], sc[f]);
+      const int unit = ((4 * lg + j) ^ l16) << 3;
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) {
+        const h8_t xh = *reinterpret_cast<const h8_t*>(xb + (16 * tj + l16) * KC + unit);
+#pragma unroll
+        for (int f = 0; f < WF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xh, acc[f][tj]);
+      }
+    }
+  };
+
+  load_w(0);
+  load_x(0, 0);
+  if constexpr (C > 1) {
+    load_w(1);
+    load_x(1, 1);
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    // nothing moves between chunks (the compiler's own waits for the weight
+    // registers do not count the copies, so hoisting chunk c + 1's dequant
+    // into chunk c would make it wait for copies just issued)
+    __builtin_amdgcn_sched_barrier(0);
+    // This wave's copies of chunk c have landed once no more vector memory
+    // instructions are outstanding than were issued after them: chunk
+    // c + 1's (s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
+    // at their maxima, i.e. not waited on).
+    if (c + 1 < C) {
+      static_assert(VM_PER_CHUNK < 64, "vmcnt is 6 bits");
+      __builtin_amdgcn_s_waitcnt((VM_PER_CHUNK & 15) | (7 << 4) | (15 << 8) | ((VM_PER_CHUNK >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    }
+    // every wave's copies too; and buffer (c + 2) % 3 was last read by
+    // compute(c - 1). The fences are LDS-only: __syncthreads' full fence
+    // would also wait for the weight loads of the chunks in flight.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    if (c + 2 < C) {
+      load_w(c + 2);
+      load_x(c + 2, (c + 2) % 3);
+    }
+    compute(c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- epilogue: lane holds o[token 16 tj + l16][ncol[f] .. + 3]
+  u2_t gw[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) gw[f] = *reinterpret_cast<const u2_t*>(gamma + ncol[f]);
+  u2_t hs[WF][TJ];   // h2 (fp16)
+  float ss[TJ];
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    ss[tj] = 0.0f;
+    const int t = min(16 * tj + l16, rows - 1);  // rows past the tile repeat the last (never stored)
+    const size_t base = (size_t)(row0 + t) * RN_BN;
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+      const float ov[4] = {acc[f][tj][0], acc[f][tj][1], acc[f][tj][2], acc[f][tj][3]};
+      const h4_t o16 = __builtin_bit_cast(h4_t, to_f16x4_native(ov));
+      const h4_t r16 = __builtin_bit_cast(h4_t, *reinterpret_cast<const u2_t*>(resid + base + ncol[f]));
+      float sv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = (float)o16[r] + (float)r16[r];
+        ss[tj] = fmaf(sv[r], sv[r], ss[tj]);
+      }
+      hs[f][tj] = to_f16x4_native(sv);
+    }
+  }
+  // row sums of squares: the 4 lane groups, then the 8 waves (fixed order)
+  float* red = reinterpret_cast<float*>(xs_lds);  // [NW8][BT]
+  __syncthreads();  // every wave is done with the activation buffers
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    float v = ss[tj];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (lg == 0) red[wave * BT + 16 * tj + l16] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    const int t = 16 * tj + l16;
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW8; ++w) tot += red[w * BT + t];
+    const float inv_rms = 1.0f / sqrtf(tot * (1.0f / (float)RN_BN) + eps);
+    if (t < rows) {
+      const size_t base = (size_t)(row0 + t) * RN_BN;
+#pragma unroll
+      for (int f = 0; f < WF; ++f) {
+        const h4_t hv = __builtin_bit_cast(h4_t, hs[f][tj]);
+        const h4_t gm = __builtin_bit_cast(h4_t, gw[f]);
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = (float)hv[r] * inv_rms * (float)gm[r];
+        *reinterpret_cast<u2_t*>(h_out + base + ncol[f]) = hs[f][tj];
+        *reinterpret_cast<u2_t*>(xn_out + base + ncol[f]) = to_f16x4_native(y);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* resid, const uint16_t* gamma,
+                         uint16_t* h_out, uint16_t* xn_out, float eps) {
+  PF_CHECK(a.N == RN_BN, "gemm_w4_add_rmsnorm: N must be 640 (one workgroup per whole row)");
+  PF_CHECK(a.K > 0 && a.K % KC == 0, "gemm_w4_add_rmsnorm: K must be a positive multiple of 128");
+  PF_CHECK(a.x && a.w && a.wsz && resid && gamma && h_out && xn_out, "gemm_w4_add_rmsnorm: null operand");
+  PF_CHECK(a.ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+               (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
+           "gemm_w4_add_rmsnorm: activations and weights must be 16-byte aligned");
+  PF_CHECK(((reinterpret_cast<uintptr_t>(resid) | reinterpret_cast<uintptr_t>(gamma) |
+             reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(xn_out) |
+             reinterpret_cast<uintptr_t>(a.bias)) & 7) == 0,
+           "gemm_w4_add_rmsnorm: residual, gamma, bias and outputs must be 8-byte aligned");
+  PF_CHECK(a.M >= 0 && (long)a.M * a.ldx < (1L << 31), "gemm_w4_add_rmsnorm: activation offsets exceed 32 bits");
+  if (a.M == 0) return;
+  const int grid = (a.M + RN_BT - 1) / RN_BT;
+  const size_t lds = std::max((size_t)3 * RN_BT * KC * sizeof(uint16_t), (size_t)RN_NW * RN_BT * sizeof(float));
+  auto go = [&](auto kern) {
+    static bool attr_set = false;  // per instance
+    if (!attr_set) {
+      PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)lds));
+      attr_set = true;
+    }
+    ProfScope ps(b, "gemm_o_add_rmsnorm");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * RN_NW), lds, b->stream, a, resid, gamma, h_out,
+                       xn_out, eps);
+    PF_HIP(hipGetLastError());
+  };
+  switch (a.K / KC) {
+    case 5: return go(&k_gemm_w4_rownorm<5>);
+    case 7: return go(&k_gemm_w4_rownorm<7>);
+    default: throw Error("gemm_w4_add_rmsnorm: K must be 640 or 896");
+  }
+}
+
 void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const uint8_t* wz, uint32_t* w_out,
                 uint32_t* sz_out, int rows, int K) {
   PF_CHECK(rows > 0 && K > 0 && K % 32 == 0, "w4_prepare: bad shape");

@@ -135,6 +135,11 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
 // K % 128 == 0. tile_t x wf selects the tile (BT tokens x 64*wf rows).
 void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t, int wf,
              const char* prof_name);
+// O projection (gemm_w4 weights, N == 640, bias folded as in gemm_w4) with the
+// residual add and RMSNorm fused: h_out = fp16(fp16(x.w + bias) + resid),
+// xn_out = fp16(h_out * inv_rms * gamma) (fp16 numerics).
+void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* resid, const uint16_t* gamma,
+                         uint16_t* h_out, uint16_t* xn_out, float eps);
 // MatMulNBits weight [rows][K/2] + scales + zero-points -> the gemm_w4 form:
 // w_out [rows][K/8] repacked dwords, sz_out [rows][K/32] (offset, scale) pairs.
 void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const uint8_t* wz, uint32_t* w_out,
