@@ -373,6 +373,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       }
     }
     record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
+    record_tap(m, "xn2." + tag, s.xn_hi, (size_t)M * D * 2);
     {
       GemmArgs a;
       a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
