@@ -25,6 +25,7 @@ Modes beside the default:
                             files into the traffic summary (markdown)
 """
 import argparse
+import subprocess
 import json
 import os
 import sys
@@ -164,6 +165,65 @@ def attention_flops(cfg, B, T):
     return 4.0 * cfg.head_dim * cfg.num_heads * B * float(keys.sum())
 
 
+BLAS_SHAPES = [  # (kernel of this build, what its launch also does)
+    ("gemm_qkv_rope", "int4 W, bias, RoPE"),
+    ("gemm_o_add_rmsnorm", "int4 W, bias, residual add, RMSNorm"),
+    ("gemm_router", "int4 W, bias, f32 out, top-4 + softmax"),
+    ("gemm_moe_gate_up", "int4 W, 128 experts grouped, bias, SwiGLU"),
+    ("gemm_moe_down", "int4 W, 128 experts grouped, bias, f32 out"),
+]
+
+
+def blas_shapes(cfg, M):
+    D, F, E, K = cfg.hidden_size, cfg.intermediate_size, cfg.num_experts, cfg.num_experts_per_tok
+    hq, hk, hd = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    S = M * K
+    return {"gemm_qkv_rope": (M, (hq + 2 * hk) * hd, D), "gemm_o_add_rmsnorm": (M, D, hq * hd),
+            "gemm_router": (M, E, D), "gemm_moe_gate_up": (S, 2 * F, D), "gemm_moe_down": (S, D, F)}
+
+
+def blas_torch_times(cfg, M, reps=20):
+    """torch.matmul of a dense fp16 [M, K] x [K, N] product (hipBLASLt on
+    ROCm; fp16 weights, no dequantisation, no expert grouping, fp16 output)
+    for each forward GEMM shape: {kernel: average us}. Runs in its own
+    process (torch's HIP runtime and the library's are separate)."""
+    import torch
+    dev = torch.device("cuda")
+    out = {}
+    for name, (m, n, k) in blas_shapes(cfg, M).items():
+        a = torch.randn(m, k, device=dev, dtype=torch.float16)
+        w = torch.randn(n, k, device=dev, dtype=torch.float16)
+        for _ in range(3):
+            torch.matmul(a, w.t())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            torch.matmul(a, w.t())
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1000.0 / reps
+        del a, w
+    return out
+
+
+def blas_reference_table(cfg, M, prof, ref):
+    """Each GEMM of the forward (its profiled average launch time, epilogue
+    included) next to the dense fp16 torch.matmul of the same M x N x K."""
+    rows = ["| kernel (this build) | its launch also does | M x N x K | this build us | TFLOP/s | "
+            "torch.matmul fp16 us | TFLOP/s | torch / this |", "|---|---|---|---|---|---|---|---|"]
+    shapes = blas_shapes(cfg, M)
+    for name, what in BLAS_SHAPES:
+        m, n, k = shapes[name]
+        fl = 2.0 * m * n * k
+        ours = prof.get(name)
+        us = ours[1] * 1000.0 / ours[0] if ours else float("nan")
+        us_ref = ref[name]
+        rows.append(f"| `{name}` | {what} | {m} x {n} x {k} | {us:.1f} | {fl / us / 1e6:.0f} | {us_ref:.1f} | "
+                    f"{fl / us_ref / 1e6:.0f} | {us_ref / us:.2f} |")
+    return "\n".join(rows)
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -189,7 +249,24 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--copy-mb", type=int, default=1024)
+    ap.add_argument("--blas-reference", action="store_true",
+                    help="print a table of each forward GEMM next to a dense fp16 torch.matmul (hipBLASLt) of "
+                         "the same M x N x K, then exit")
+    ap.add_argument("--blas-torch", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+
+    if args.blas_torch:  # the torch half of --blas-reference, in a process of its own
+        from textsift_amd.config import PF_CONFIG
+        print(json.dumps(blas_torch_times(PF_CONFIG, args.batch * args.seq)))
+        return
+    blas_ref = None
+    if args.blas_reference:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--blas-torch", "--batch", str(args.batch),
+                            "--seq", str(args.seq)], capture_output=True, text=True)
+        if r.returncode != 0:
+            print(r.stderr, file=sys.stderr)
+            sys.exit(r.returncode)
+        blas_ref = json.loads(r.stdout.strip().splitlines()[-1])
 
     if args.traffic_report:
         print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb))
@@ -251,6 +328,10 @@ def main():
     be.profile_select(None)
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
     tok_s = M / (ms_per_step / 1000.0)
+
+    if args.blas_reference:
+        print(blas_reference_table(cfg, M, prof, blas_ref))
+        return
 
     # sanity: logits finite
     logits = logits_buf.read(np.float32)
