@@ -113,7 +113,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int t0 = blockIdx.x * QB;
-  const int g = blockIdx.y;                  // kv head
+  const int g = blockIdx.y / a.head_groups;  // kv head
+  const int hgrp = blockIdx.y % a.head_groups;  // which of its query heads this workgroup takes
   const int bseq = blockIdx.z;
   const int T = a.T, W = a.window;
   const size_t seq0 = (size_t)bseq * T;
@@ -140,9 +141,10 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int any_hi = wave_max_i(q_ok ? hi0 : 0);
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
+  const int GH = G / a.head_groups;          // query heads per workgroup
   const float sscale = a.scale;
 
-  for (int hh = 0; hh < G; ++hh) {
+  for (int hh = hgrp * GH; hh < (hgrp + 1) * GH; ++hh) {
     const int hq = g * G + hh;
     // Opaque per-head copies of the window bounds: comparisons against them
     // are then recomputed per head instead of being hoisted out of the loop
@@ -308,7 +310,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int t0 = blockIdx.x * QB;
-  const int g = blockIdx.y;                  // kv head
+  const int g = blockIdx.y / a.head_groups;  // kv head
+  const int hgrp = blockIdx.y % a.head_groups;  // which of its query heads this workgroup takes
   const int bseq = blockIdx.z;
   const int T = a.T, W = a.window;
   const size_t seq0 = (size_t)bseq * T;
@@ -327,12 +330,17 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   // wave-uniform: chunks wholly inside every lane's window (lanes past T do not constrain them)
   const int full_lo = wave_max_i(q_ok ? lo0 : 0);
   const int full_hi = wave_min_i(q_ok ? hi0 : 1 << 20);
+  // chunks outside every lane's window (near the sequence ends) are skipped
+  const int any_lo = wave_min_i(q_ok ? lo0 : 1 << 20);
+  const int any_hi = wave_max_i(q_ok ? hi0 : -1);
+  auto empty = [&](int c) { return 32 * c + 32 <= any_lo || 32 * c >= any_hi; };
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
+  const int GH = G / a.head_groups;          // query heads per workgroup
   constexpr float LOG2_E = 1.44269504088896340736f;
   const float sscale = a.scale * LOG2_E;     // scores in the exponent's units
 
-  for (int hh = 0; hh < G; ++hh) {
+  for (int hh = hgrp * GH; hh < (hgrp + 1) * GH; ++hh) {
     const int hq = g * G + hh;
     // opaque per-head copies of the window bounds (see k_banded_attention)
     int lo = lo0, hi = hi0;
@@ -364,13 +372,20 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     for (int c = 0; c < NCH; ++c) {
       if (c + 1 < NCH) load_k(c + 1, kn);
       f4_t acc[2];
+      if (!empty(c)) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][0], qf[0], f4_t{0.f, 0.f, 0.f, 0.f});
+        for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][0], qf[0], f4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int dh = 1; dh < NDH; ++dh)
+        for (int dh = 1; dh < NDH; ++dh)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][dh], qf[dh], acc[kt]);
-      if (!masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi) {
+          for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][dh], qf[dh], acc[kt]);
+      }
+      if (empty(c)) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[c][kt][r] = -INFINITY;
+      } else if (!masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -435,27 +450,29 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     for (int c = 0; c < NCH; ++c) {
       if (c + 1 < NCH) load_v(c + 1, vn);
       h8_t ph, pl;
+      if (!empty(c)) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
-          const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
-          const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
-          const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
-          const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
-          const h2_t hl = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
-          ph[4 * kt + r] = hh[0];
-          ph[4 * kt + r + 1] = hh[1];
-          pl[4 * kt + r] = hl[0];
-          pl[4 * kt + r + 1] = hl[1];
-        }
+          for (int r = 0; r < 4; r += 2) {
+            const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
+            const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
+            const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
+            const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
+            const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+            const h2_t hl = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
+            ph[4 * kt + r] = hh[0];
+            ph[4 * kt + r + 1] = hh[1];
+            pl[4 * kt + r] = hl[0];
+            pl[4 * kt + r + 1] = hl[1];
+          }
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
-      lsum = mfma16x16x32(ones, ph, lsum);
+        for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
+        lsum = mfma16x16x32(ones, ph, lsum);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
-      lsum = mfma16x16x32(ones, pl, lsum);
+        for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
+        lsum = mfma16x16x32(ones, pl, lsum);
+      }
       if (c + 1 < NCH) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) vf[dt] = vn[dt];
@@ -483,9 +500,14 @@ void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, size_t lds, 
                                (int)lds));
     attr_set = true;
   }
-  dim3 grid((a.T + qb - 1) / qb, a.Hkv, a.B);
+  // few workgroups (short inputs): one per query head instead of one per KV
+  // head group, so the heads run in parallel
+  AttnArgs g = a;
+  const long wgs = (long)((a.T + qb - 1) / qb) * a.Hkv * a.B;
+  g.head_groups = wgs < b->num_cus ? a.Hq / a.Hkv : 1;
+  dim3 grid((a.T + qb - 1) / qb, a.Hkv * g.head_groups, a.B);
   ProfScope ps(b, "banded_attention");
-  hipLaunchKernelGGL(kern, grid, dim3(nt), lds, b->stream, a);
+  hipLaunchKernelGGL(kern, grid, dim3(nt), lds, b->stream, g);
   PF_HIP(hipGetLastError());
 }
 
