@@ -22,26 +22,34 @@ constexpr int ROWS_PER_BLOCK = 4;  // one wave per row, 4 waves per block
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
                                                const uint8_t* __restrict__ zp, const int32_t* __restrict__ ids,
                                                uint16_t* __restrict__ out, int T, int V, int D) {
-  const int gpr = D >> 3;  // 8-value groups per row
+  // one thread per quant block: 16 bytes of nibbles, its scale and zero-point
+  // -> 32 fp16 values (64 contiguous output bytes); consecutive threads take
+  // consecutive blocks of a row, so loads and stores are contiguous per row
+  const int nb = D >> 5;
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)T * gpr) return;
-  const int t = (int)(i / gpr), g = (int)(i % gpr);
-  const int nb = D >> 5, blk = g >> 2;
+  if (i >= (size_t)T * nb) return;
+  const int t = (int)(i / nb), blk = (int)(i % nb);
   const int id = ids[t];
-  u4_t res = {0u, 0u, 0u, 0u};
+  u4_t res[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
   if (id >= 0 && id < V) {
     const size_t row = (size_t)id;
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(q + row * (D >> 1) + g * 4);
+    const u4_t w = *reinterpret_cast<const u4_t*>(q + row * (D >> 1) + blk * 16);
     const float sc = wasm_h2f(s[row * nb + blk]);
     const uint8_t zb = zp[row * ((nb + 1) >> 1) + (blk >> 1)];
     const int z = (blk & 1) ? (zb >> 4) : (zb & 0xF);
-    float v[8];
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (float)((int)((w >> (4 * j)) & 0xFu) - z) * sc;
-    const u2_t a = to_f16x4(v), c = to_f16x4(v + 4);
-    res = u4_t{a.x, a.y, c.x, c.y};
+    for (int d = 0; d < 4; ++d) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (float)((int)((wd[d] >> (4 * j)) & 0xFu) - z) * sc;
+      const u2_t a = to_f16x4(v), c = to_f16x4(v + 4);
+      res[d] = u4_t{a.x, a.y, c.x, c.y};
+    }
   }
-  *reinterpret_cast<u4_t*>(out + (size_t)t * D + g * 8) = res;
+  u4_t* o = reinterpret_cast<u4_t*>(out + (size_t)t * D + blk * 32);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = res[d];
 }
 
 // ----------------------------------------------------------------------------
@@ -774,10 +782,10 @@ void probe_fast_math(pfhip_backend* b, int which, uint32_t lo, uint32_t hi, uint
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D) {
   PF_CHECK(D > 0 && D % 32 == 0, "embed_lookup: D must be a multiple of 32");
-  PF_CHECK(((uintptr_t)q & 3) == 0 && ((uintptr_t)out & 15) == 0,
-           "embed_lookup: table must be 4-byte and output 16-byte aligned");
+  PF_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0,
+           "embed_lookup: table and output must be 16-byte aligned");
   if (T <= 0) return;
-  const size_t n = (size_t)T * (D / 8);
+  const size_t n = (size_t)T * (D / 32);
   ProfScope ps(b, "embed_lookup_int4");
   hipLaunchKernelGGL(k_embed, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, b->stream, q, s, zp, ids, out, T, V,
                      D);
