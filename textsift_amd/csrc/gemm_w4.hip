@@ -93,7 +93,7 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // fragment, PS bytes one lane holds per fragment row; the tile is staged in
 // NP passes of FG fragments per wave (PRB bytes per staged row, UP 16-byte
 // units, units XOR-swizzled by row & SWM for conflict-free LDS writes).
-template <int WF, int BT, Epi EPI>
+template <int WF, int BT, Epi EPI, int NW = 4>
 struct StagedOut {
   static constexpr bool F32OUT = EPI == Epi::F32 || EPI == Epi::F32_TOPK;
   static constexpr bool OK = F32OUT || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16;
@@ -107,14 +107,18 @@ struct StagedOut {
   static constexpr int UP = PRB / 16;
   static constexpr int SWM = UP % 16 == 0 ? 15 : (UP % 8 == 0 ? 7 : (UP % 4 == 0 ? 3 : 0));
   static constexpr size_t LDS = (size_t)BT * PRB;
-  static_assert(BT * UP % 256 == 0, "staged stores: whole rounds of 256 units");
+  static_assert(BT * UP % (64 * NW) == 0, "staged stores: whole rounds of one unit per thread");
 };
 
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED>
-__global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
+// NW waves per workgroup (4: two workgroups per CU; 8 measured on a
+// 256-token tile: each dequantised fragment feeds twice the MFMAs, but the
+// doubled activation reads from LDS cancel it: gate_up -2 %, down +10 %)
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
-  constexpr int XI = BT / 16;       // 1 KB direct loads per wave per plane per chunk
+  constexpr int XI = BT / (4 * NW);  // 1 KB (4-row) direct loads per wave per plane per chunk
+  static_assert(XI >= 1 && BT % (4 * NW) == 0, "whole 4-row copies per wave");
   constexpr int PLANE = BT * KC;    // halves per plane per buffer
 
   extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [2][XS][BT][KC] swizzled
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
   }
 
   // ---- epilogue: lane holds out[token = 16 tj + l16][n = n0 + (wave WF + f) 16 + 4 lg + r]
-  using SO = StagedOut<WF, BT, EPI>;
+  using SO = StagedOut<WF, BT, EPI, NW>;
   if (SO::OK && p.out_staged) {
     // The tile goes out through LDS: lanes write their values in row-major
     // order, then every lane stores whole 16-byte units of consecutive
@@ -359,8 +363,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
       const int ocol0 = EPI == Epi::SWIGLU_F16 ? n0 / 2 : n0;
       const int oN = EPI == Epi::SWIGLU_F16 ? p.N / 2 : p.N;
 #pragma unroll
-      for (int i = 0; i < BT * SO::UP / 256; ++i) {
-        const int idx = i * 256 + tid, row = idx / SO::UP, up = idx % SO::UP;
+      for (int i = 0; i < BT * SO::UP / (64 * NW); ++i) {
+        const int idx = i * (64 * NW) + tid, row = idx / SO::UP, up = idx % SO::UP;
         const int byte = ((up ^ (row & SO::SWM)) << 4);
         const int w = byte / (SO::FG * SO::FB), within = byte % (SO::FG * SO::FB);
         const int col = ocol0 + (w * WF + ps * SO::FG) * SO::CF + within / SO::ESZ;
@@ -369,7 +373,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
               *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
       }
     }
-    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 == 256) {
+    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 == 64 * NW) {
       // Router top-4 of every row from the staged tile (all N == 128 logits
       // of BT rows are in LDS): two threads per row each take the top-4 of
       // one half by the reference's insertion rule, then the halves merge by
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_w4(GemmArgs p) {
   }
 }
 
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED>
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4>
 void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   constexpr int BN = NW * WF * 16;
   const int n_tiles = (a.N + BN - 1) / BN;
@@ -482,37 +486,41 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   if (grid == 0) return;
   PF_CHECK(grid < (1L << 31), "gemm_w4: grid too large");
   const size_t lds = std::max((size_t)2 * XS * BT * KC * sizeof(uint16_t),
-                              StagedOut<WF, BT, EPI>::OK ? StagedOut<WF, BT, EPI>::LDS : (size_t)0);
+                              StagedOut<WF, BT, EPI, NW>::OK ? StagedOut<WF, BT, EPI, NW>::LDS : (size_t)0);
   static bool attr_set = false;  // per template instance
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED>),
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
   ProfScope ps(b, name);
-  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED>), dim3((unsigned)grid), dim3(256), lds, b->stream, a);
+  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW>), dim3((unsigned)grid), dim3(64 * NW), lds, b->stream,
+                     a);
   PF_HIP(hipGetLastError());
 }
 
-template <int WF, int BT, int XS, bool GROUPED>
+template <int WF, int BT, int XS, bool GROUPED, int NW>
 void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name) {
   switch (epi) {
-    case Epi::F16: return launch<WF, BT, XS, Epi::F16, GROUPED>(b, a, name);
-    case Epi::F32: return launch<WF, BT, XS, Epi::F32, GROUPED>(b, a, name);
-    case Epi::ROPE_F16: return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED>(b, a, name);
+    case Epi::F16: return launch<WF, BT, XS, Epi::F16, GROUPED, NW>(b, a, name);
+    case Epi::F32: return launch<WF, BT, XS, Epi::F32, GROUPED, NW>(b, a, name);
+    case Epi::ROPE_F16:
+      if constexpr (NW == 4) return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED, NW>(b, a, name);
+      break;
     case Epi::SWIGLU_SPLIT: break;
-    case Epi::SWIGLU_F16: return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED>(b, a, name);
+    case Epi::SWIGLU_F16: return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED, NW>(b, a, name);
     case Epi::F32_TOPK:
-      if constexpr (WF == 2 && BT == 128 && !GROUPED) return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED>(b, a, name);
+      if constexpr (WF == 2 && BT == 128 && !GROUPED && NW == 4)
+        return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW>(b, a, name);
       break;
   }
-  throw Error("gemm_w4: unsupported epilogue");
+  throw Error("gemm_w4: unsupported epilogue for this tile");
 }
 
-template <int WF, int BT>
+template <int WF, int BT, int NW = 4>
 void dispatch_grouped(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped, const char* name) {
-  if (grouped) dispatch_epi<WF, BT, 1, true>(b, a, epi, name);
-  else dispatch_epi<WF, BT, 1, false>(b, a, epi, name);
+  if (grouped) dispatch_epi<WF, BT, 1, true, NW>(b, a, epi, name);
+  else dispatch_epi<WF, BT, 1, false, NW>(b, a, epi, name);
 }
 
 // ---------------------------------------------------------------- weight prep
