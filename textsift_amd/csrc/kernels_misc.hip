@@ -483,7 +483,9 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
 // The reference weights by softmax/K and rescales by K at the end; both are
 // exact powers of two, so weighting by the softmax directly is bit-identical.
 // NMODE: -1 = no norm; OUT_F16 / OUT_SPLIT = form of the next block's norm output.
-template <int NMODE, int K>
+// NJ 256-element slices per row (3 covers D <= 768 with fewer registers
+// than the general 4, so more waves stay resident).
+template <int NMODE, int K, int NJ = MAXJ>
 __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                      const int32_t* __restrict__ slot_of, const float* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
@@ -519,10 +521,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     }
   const size_t base = (size_t)t * D;
   // every load of the row is issued before any is used
-  f4_t yv[MAXJ][K];
-  u2_t rw[MAXJ], gw[MAXJ];
+  f4_t yv[NJ][K];
+  u2_t rw[NJ], gw[NJ];
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int d = 4 * lane + 256 * j;
     if (d < D) {
 #pragma unroll
@@ -531,10 +533,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
       if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
     }
   }
-  u2_t hs[MAXJ];
+  u2_t hs[NJ];
   float ss = 0.0f;
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int d = 4 * lane + 256 * j;
     hs[j] = u2_t{0u, 0u};
     if (d < D) {
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     ss = wave_sum(ss);
     const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int d = 4 * lane + 256 * j;
       if (d < D) {
         float hv[4], gm[4], yo[4];
@@ -582,6 +584,12 @@ void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const 
                     const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
                     uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
   const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  if (D <= 768 && K == 4) {  // the model's shape
+    hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
+                       moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);
+    PF_HIP(hipGetLastError());
+    return;
+  }
   switch (K) {
 #define PF_COMBINE_CASE(k)                                                                                       \
   case k:                                                                                                        \
