@@ -42,13 +42,13 @@ HBM_PEAK_GBS = 8000.0
 
 # rocprofv3 kernel symbols -> the launch names the backend profiles under
 KERNEL_LABELS = [
-    ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true>")),
-    ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true>")),
-    ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false>")),
+    ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true")),
+    ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true")),
+    ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false")),
     ("gemm_o_add_rmsnorm", ("k_gemm_w4_rownorm",)),
-    ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false>")),
-    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)5, false>")),
-    ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false>")),
+    ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false")),
+    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)5, false")),
+    ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false")),
     ("banded_attention", ("k_banded_attention",)),
     ("moe_combine_norm", ("k_moe_combine",)),
     ("add_rmsnorm_f16", ("k_add_rms_norm",)),
@@ -126,6 +126,40 @@ def traffic_report(fetch_csv, write_csv, copy_mb):
             ""] if kf and kw else ["no calibration copy found", ""]
     tail = [""] + [f"hbm_bytes_per_launch {lab}: {int(v)}" for lab, v in summary.items() if v]
     return "\n".join(head + lines + tail)
+
+
+SQ_PASS1 = "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_WAIT_INST_ANY SQ_WAIT_ANY " \
+           "SQ_ACTIVE_INST_LDS SQ_VALU_MFMA_COEXEC_CYCLES"
+SQ_PASS2 = "SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_ANY " \
+           "SQ_INSTS_SALU SQ_WAVES"
+
+
+def sq_report(p1_csv, p2_csv, cus=256, ses=32):
+    """Markdown summary of the SQ counter passes, per kernel and dispatch:
+    instructions per wave and MFMA pipe utilisation. SQ_BUSY_CYCLES sums
+    the shader engines (ses of them), SQ_VALU_MFMA_BUSY_CYCLES all SIMDs
+    (4 per CU), so MFMA busy = (MFMA_BUSY / (4 cus)) / (BUSY / ses)."""
+    names = SQ_PASS1.split() + SQ_PASS2.split()
+    per = {}
+    for path, cnts in ((p1_csv, SQ_PASS1.split()), (p2_csv, SQ_PASS2.split())):
+        for cn in cnts:
+            for d, (sym, v) in read_counters(path, cn).items():
+                lab = label_of(sym)
+                if lab:
+                    per.setdefault(lab, {}).setdefault(cn, {})[(path, d)] = v
+    lines = ["| kernel | waves | VALU / wave | MFMA / wave | SALU / wave | LDS / wave | LDS conflict cycles / LDS instr | "
+             "MFMA busy | wave time waiting on dependencies |", "|---|---|---|---|---|---|---|---|---|"]
+    for lab, _ in KERNEL_LABELS:
+        if lab not in per or any(n not in per[lab] for n in names):
+            continue
+        a = {n: sum(per[lab][n].values()) / len(per[lab][n]) for n in names}
+        w = a["SQ_WAVES"] or 1.0
+        mfma_busy = (a["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * cus)) / (a["SQ_BUSY_CYCLES"] / ses)
+        lines.append(f"| {lab} | {w:.0f} | {a['SQ_INSTS_VALU'] / w:.0f} | {a['SQ_INSTS_MFMA'] / w:.0f} | "
+                     f"{a['SQ_INSTS_SALU'] / w:.0f} | {a['SQ_INSTS_LDS'] / w:.0f} | "
+                     f"{a['SQ_LDS_BANK_CONFLICT'] / max(a['SQ_INSTS_LDS'], 1.0):.1f} | {100 * mfma_busy:.0f} % | "
+                     f"{100 * a['SQ_WAIT_INST_ANY'] / a['SQ_WAVE_CYCLES']:.0f} % |")
+    return "\n".join(lines)
 
 
 def read_traffic(kernel):
@@ -249,6 +283,8 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--copy-mb", type=int, default=1024)
+    ap.add_argument("--sq-report", nargs=2, metavar=("PASS1_CSV", "PASS2_CSV"),
+                    help="summarise two rocprofv3 --pmc passes of the counters in SQ_PASS1 / SQ_PASS2")
     ap.add_argument("--blas-reference", action="store_true",
                     help="print a table of each forward GEMM next to a dense fp16 torch.matmul (hipBLASLt) of "
                          "the same M x N x K, then exit")
@@ -270,6 +306,9 @@ def main():
 
     if args.traffic_report:
         print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb))
+        return
+    if args.sq_report:
+        print(sq_report(args.sq_report[0], args.sq_report[1]))
         return
 
     if args.gpus != 1:
