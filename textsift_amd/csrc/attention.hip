@@ -359,7 +359,9 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     // fragments of chunk c + 1 are read while chunk c is processed.
     float s[NCH][2][4];
     float mr = -INFINITY;
-    h8_t kf[2][NDH], kn[2][NDH];
+    // K fragments double-buffered by chunk parity (compile-time indices once
+    // the chunk loop is unrolled: no register copies between chunks)
+    h8_t kb[2][2][NDH];
     auto load_k = [&](int c, h8_t (&dst)[2][NDH]) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -367,10 +369,11 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         for (int dh = 0; dh < NDH; ++dh)
           dst[kt][dh] = *reinterpret_cast<const h8_t*>(&Ks[(rb + 32 * c + 16 * kt + l16) * LDK + 32 * dh + 8 * lg]);
     };
-    load_k(0, kf);
+    load_k(0, kb[0]);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      if (c + 1 < NCH) load_k(c + 1, kn);
+      if (c + 1 < NCH) load_k(c + 1, kb[(c + 1) & 1]);
+      const h8_t (&kf)[2][NDH] = kb[c & 1];
       f4_t acc[2];
       if (!empty(c)) {
 #pragma unroll
@@ -405,12 +408,6 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
             mr = fmaxf(mr, sv);
           }
       }
-      if (c + 1 < NCH) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int dh = 0; dh < NDH; ++dh) kf[kt][dh] = kn[kt][dh];
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
     // lanes l, l^16, l^32, l^48 hold the same query
@@ -435,7 +432,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     f4_t o[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[dt] = f4_t{0.f, 0.f, 0.f, 0.f};
-    h8_t vf[NDT], vn[NDT];
+    h8_t vb[2][NDT];  // V^T fragments double-buffered by chunk parity
     auto load_v = [&](int c, h8_t (&dst)[NDT]) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
@@ -445,39 +442,57 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         dst[dt] = h8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
       }
     };
-    load_v(0, vf);
+    // e of chunk c as fp16 hi (ph) and lo (pl) B operands
+    auto split = [&](int c, h8_t& ph, h8_t& pl) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (c + 1 < NCH) load_v(c + 1, vn);
-      h8_t ph, pl;
-      if (!empty(c)) {
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int r = 0; r < 4; r += 2) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
+          const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
+          const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
+          const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+          const h2_t hl = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
+          ph[4 * kt + r] = hh[0];
+          ph[4 * kt + r + 1] = hh[1];
+          pl[4 * kt + r] = hl[0];
+          pl[4 * kt + r + 1] = hl[1];
+        }
+    };
+    auto pv = [&](const h8_t (&vf)[NDT], const h8_t& ph, const h8_t& pl) {
 #pragma unroll
-          for (int r = 0; r < 4; r += 2) {
-            const float e0 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r], sscale, nm));
-            const float e1 = __builtin_amdgcn_exp2f(fmaf(s[c][kt][r + 1], sscale, nm));
-            const float h0 = __uint_as_float(__float_as_uint(e0) & 0xFFFFE000u);
-            const float h1 = __uint_as_float(__float_as_uint(e1) & 0xFFFFE000u);
-            const h2_t hh = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(h0, h1));
-            const h2_t hl = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
-            ph[4 * kt + r] = hh[0];
-            ph[4 * kt + r + 1] = hh[1];
-            pl[4 * kt + r] = hl[0];
-            pl[4 * kt + r + 1] = hl[1];
-          }
+      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
+      lsum = mfma16x16x32(ones, ph, lsum);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], ph, o[dt]);
-        lsum = mfma16x16x32(ones, ph, lsum);
+      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
+      lsum = mfma16x16x32(ones, pl, lsum);
+    };
+    load_v(0, vb[0]);
+    if (!empty(0) && !empty(NCH - 1)) {
+      // every chunk has keys (all but the sequence ends): one branch-free
+      // block in which chunk c + 1's exponentials are computed before chunk
+      // c's MFMAs are issued, so the compiler can interleave the two
+      h8_t pb[2][2];  // [parity][hi, lo]
+      split(0, pb[0][0], pb[0][1]);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pl, o[dt]);
-        lsum = mfma16x16x32(ones, pl, lsum);
+      for (int c = 0; c < NCH; ++c) {
+        if (c + 1 < NCH) {
+          load_v(c + 1, vb[(c + 1) & 1]);
+          split(c + 1, pb[(c + 1) & 1][0], pb[(c + 1) & 1][1]);
+        }
+        pv(vb[c & 1], pb[c & 1][0], pb[c & 1][1]);
       }
-      if (c + 1 < NCH) {
+    } else {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) vf[dt] = vn[dt];
+      for (int c = 0; c < NCH; ++c) {
+        if (c + 1 < NCH) load_v(c + 1, vb[(c + 1) & 1]);
+        if (!empty(c)) {
+          h8_t ph, pl;
+          split(c, ph, pl);
+          pv(vb[c & 1], ph, pl);
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     const float l = lsum[0] + __builtin_amdgcn_exp2f(sink - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
