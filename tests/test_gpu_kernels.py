@@ -334,7 +334,10 @@ def test_attention_fixture(be, fixture):
 @pytest.mark.parametrize("T,W,masked,sinks", [(8192, 128, False, False),
                                               (2048, 128, True, True),     # model shape, mask + sinks
                                               (77, 128, False, True),      # T < window
-                                              (200, 5, True, False)])
+                                              (200, 5, True, False),
+                                              # enough workgroups (256 x 128 queries x 2 KV heads) for the
+                                              # launcher's one-workgroup-per-KV-head form (the 16 x 2048 one)
+                                              (16384, 128, False, True)])
 def test_attention_vs_oracle(be, T, W, masked, sinks, hw_exp):
     """hw_exp=1 is the fp16 forward's softmax (hardware exp2, as the
     reference's GPU shader uses exp), checked against the shader's
