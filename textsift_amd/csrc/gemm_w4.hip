@@ -620,6 +620,12 @@ namespace {
 
 constexpr int RN_NW = 8, RN_WF = 5, RN_BT = 64;
 constexpr int RN_BN = RN_NW * RN_WF * 16;  // 640
+// chunks loaded ahead of the one computed, and activation buffers: two
+// ahead for 64-row tiles; one for 128-row tiles, whose chunks carry twice
+// the MFMAs. (128-row tiles do not fit: 160 accumulator registers plus the
+// weight sets and addresses exceed 256 and spill.)
+constexpr int RN_PD = RN_BT <= 64 ? 2 : 1;
+constexpr int RN_NB = RN_PD + 1;
 
 // copy16_to_lds issued as inline assembly: the compiler then does not know
 // that it writes LDS and does not make every workgroup barrier wait for all
@@ -645,7 +651,8 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   // vector memory instructions per lane and chunk, issued in this order:
   // WF weight and WF scale loads, then XI activation copies
   constexpr int VM_PER_CHUNK = 2 * WF + XI;
-  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [3][BT][KC] swizzled, then the row sums
+  constexpr int PD = RN_PD, NB = RN_NB;
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [NB][BT][KC] swizzled, then the row sums
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -680,7 +687,7 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
       copy16_to_lds_async(xsrc + xoff[m] + c * KC,
                           __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(buf * PLANE + (m * NW8 + wave) * 512) * 2));
   };
-  u4_t wraw[C][WF];  // only three chunks' sets are live at a time
+  u4_t wraw[C][WF];  // only PD + 1 chunks' sets are live at a time
   uint32_t sz[C][WF];
   auto load_w = [&](int c) {
 #pragma unroll
@@ -714,7 +721,7 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
       off[f] = h2_t{pr.x, pr.x};
       sc[f] = h2_t{pr.y, pr.y};
     }
-    const _Float16* xb = xs_lds + (c % 3) * PLANE;
+    const _Float16* xb = xs_lds + (c % NB) * PLANE;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
@@ -730,11 +737,10 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     }
   };
 
-  load_w(0);
-  load_x(0, 0);
-  if constexpr (C > 1) {
-    load_w(1);
-    load_x(1, 1);
+#pragma unroll
+  for (int i = 0; i < PD && i < C; ++i) {
+    load_w(i);
+    load_x(i, i);
   }
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -743,24 +749,24 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     // into chunk c would make it wait for copies just issued)
     __builtin_amdgcn_sched_barrier(0);
     // This wave's copies of chunk c have landed once no more vector memory
-    // instructions are outstanding than were issued after them: chunk
-    // c + 1's (s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt
-    // at their maxima, i.e. not waited on).
-    if (c + 1 < C) {
-      static_assert(VM_PER_CHUNK < 64, "vmcnt is 6 bits");
+    // instructions are outstanding than were issued after them: those of
+    // chunks c + 1 .. c + PD - 1 (s_waitcnt: vmcnt in bits 3:0 and 15:14;
+    // expcnt and lgkmcnt at their maxima, i.e. not waited on).
+    static_assert(VM_PER_CHUNK < 64 && PD <= 2, "vmcnt is 6 bits");
+    if (PD == 2 && c + 1 < C) {
       __builtin_amdgcn_s_waitcnt((VM_PER_CHUNK & 15) | (7 << 4) | (15 << 8) | ((VM_PER_CHUNK >> 4) << 14));
     } else {
       __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     }
-    // every wave's copies too; and buffer (c + 2) % 3 was last read by
+    // every wave's copies too; and buffer (c + PD) % NB was last read by
     // compute(c - 1). The fences are LDS-only: __syncthreads' full fence
     // would also wait for the weight loads of the chunks in flight.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    if (c + 2 < C) {
-      load_w(c + 2);
-      load_x(c + 2, (c + 2) % 3);
+    if (c + PD < C) {
+      load_w(c + PD);
+      load_x(c + PD, (c + PD) % NB);
     }
     compute(c);
   }
@@ -772,16 +778,24 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   for (int f = 0; f < WF; ++f) gw[f] = *reinterpret_cast<const u2_t*>(gamma + ncol[f]);
   u2_t hs[WF][TJ];   // h2 (fp16)
   float ss[TJ];
+  // residual rows one token fragment ahead (all at once would not fit the registers)
+  u2_t rres[2][WF];
+  auto load_res = [&](int tj, u2_t (&dst)[WF]) {
+    const int t = min(16 * tj + l16, rows - 1);  // rows past the tile repeat the last (never stored)
+#pragma unroll
+    for (int f = 0; f < WF; ++f)
+      dst[f] = *reinterpret_cast<const u2_t*>(resid + (size_t)(row0 + t) * RN_BN + ncol[f]);
+  };
+  load_res(0, rres[0]);
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj) {
+    if (tj + 1 < TJ) load_res(tj + 1, rres[(tj + 1) & 1]);
     ss[tj] = 0.0f;
-    const int t = min(16 * tj + l16, rows - 1);  // rows past the tile repeat the last (never stored)
-    const size_t base = (size_t)(row0 + t) * RN_BN;
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
       const float ov[4] = {acc[f][tj][0], acc[f][tj][1], acc[f][tj][2], acc[f][tj][3]};
       const h4_t o16 = __builtin_bit_cast(h4_t, to_f16x4_native(ov));
-      const h4_t r16 = __builtin_bit_cast(h4_t, *reinterpret_cast<const u2_t*>(resid + base + ncol[f]));
+      const h4_t r16 = __builtin_bit_cast(h4_t, rres[tj & 1][f]);
       float sv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -790,6 +804,7 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
       }
       hs[f][tj] = to_f16x4_native(sv);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
   // row sums of squares: the 4 lane groups, then the 8 waves (fixed order)
   float* red = reinterpret_cast<float*>(xs_lds);  // [NW8][BT]
@@ -842,7 +857,7 @@ void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* re
   PF_CHECK(a.M >= 0 && (long)a.M * a.ldx < (1L << 31), "gemm_w4_add_rmsnorm: activation offsets exceed 32 bits");
   if (a.M == 0) return;
   const int grid = (a.M + RN_BT - 1) / RN_BT;
-  const size_t lds = std::max((size_t)3 * RN_BT * KC * sizeof(uint16_t), (size_t)RN_NW * RN_BT * sizeof(float));
+  const size_t lds = std::max((size_t)RN_NB * RN_BT * KC * sizeof(uint16_t), (size_t)RN_NW * RN_BT * sizeof(float));
   auto go = [&](auto kern) {
     static bool attr_set = false;  // per instance
     if (!attr_set) {
