@@ -289,32 +289,35 @@ def test_fused_router_topk_bit_exact(kind):
     assert np.allclose(rw, w_ref, rtol=0.0, atol=2e-7, equal_nan=True)
 
 
-def test_fused_o_residual_norm_vs_oracle(small):
-    """The O projection with the residual add and RMSNorm in its epilogue
-    (fp16 numerics): the new residual h2 and the normalised xn against the
-    oracle's MatMulNBits (fp16 out, zig/wasm_exports.zig:560-707) and
-    add_rmsnorm (:288-350) on the same inputs (the GPU's attention output
-    and the block's input, the embedding)."""
+@pytest.mark.parametrize("B,T", [(1, 300), (8, 2048)], ids=["two-kernels", "fused"])
+def test_o_residual_norm_vs_oracle(small, B, T):
+    """The O projection, residual add and RMSNorm (fp16 numerics): as the O
+    GEMM and add_rmsnorm kernels for small batches, as one kernel with the
+    add and the norm in its epilogue from 16384 rows on. The new residual h2
+    and the normalised xn against the oracle's MatMulNBits (fp16 out,
+    zig/wasm_exports.zig:560-707) and add_rmsnorm (:288-350) on the same
+    inputs (the GPU's attention output and the block's input, the embedding)."""
     w, be = small
     if be.precision != _native.PRECISION_FP16:
-        pytest.skip("the fused epilogue is the fp16 path")
-    T, D = 300, PF_CONFIG.hidden_size
-    ids = synth.token_ids(903, T, V)
+        pytest.skip("the fp16 path")
+    D, M = PF_CONFIG.hidden_size, B * T
+    ids = synth.token_ids(903, M, V)
     m = be.model
     m.enable_taps(True)
-    be.forward(ids, np.ones(T, np.uint8))
-    att = m.tap("att.0", np.uint16, T * 896).reshape(T, 896)
-    h2 = m.tap("h2.0", np.uint16, T * D).reshape(T, D)
-    xn = m.tap("xn2.0", np.uint16, T * D).reshape(T, D)
+    be.forward_batch(ids.reshape(B, T))
+    att = m.tap("att.0", np.uint16, M * 896).reshape(M, 896)
+    h2 = m.tap("h2.0", np.uint16, M * D).reshape(M, D)
+    xn = m.tap("xn2.0", np.uint16, M * D).reshape(M, D)
     m.enable_taps(False)
     h_in = oracle.embed_lookup(w["embed.int4"], w["embed.scales"], w["embed.zp"], ids, V, D)
     pre = "layers.0.attn.o_proj"
     o_ref = oracle.matmul(att, w[f"{pre}.int4"], w[f"{pre}.scales"], w[f"{pre}.zp"], w[f"{pre}.bias"], D, 896,
                           False, False)
-    s_ref, n_ref = oracle.add_rmsnorm_f32(h_in, o_ref, w["layers.0.post_attention_layernorm"], T, D,
+    s_ref, n_ref = oracle.add_rmsnorm_f32(h_in, o_ref, w["layers.0.post_attention_layernorm"], M, D,
                                           PF_CONFIG.rms_norm_eps)
     e_h, e_n = rel_err_norm(f16(h2), f16(s_ref)), rel_err_norm(f16(xn), n_ref)
-    print(f"fused O + add + norm: h2 rel-err {e_h:.3e} (identical {np.mean(h2 == s_ref):.4f}), xn rel-err {e_n:.3e}")
+    print(f"O + add + norm B={B} T={T}: h2 rel-err {e_h:.3e} (identical {np.mean(h2 == s_ref):.4f}), "
+          f"xn rel-err {e_n:.3e}")
     assert e_h < 2e-3 and e_n < 2e-3
     # the scale-folded fp16 weights move o by ~2^-12 relative, which changes
     # the fp16 rounding of about a fifth of the sums
