@@ -258,6 +258,43 @@ def blas_reference_table(cfg, M, prof, ref):
     return "\n".join(rows)
 
 
+# The reference's published single-sequence forward latencies (ms) at small T
+# (its README.md:172-184 and docs-site/src/content/docs/benchmarks.mdx:14-39):
+# WebGPU on an Apple M3 Pro, Metal-direct on an Apple M2 Pro, synthetic weights.
+REF_LATENCY_MS = {7: {"WebGPU M3 Pro": 8.9, "Metal M2 Pro": 5.2}, 25: {"WebGPU M3 Pro": 11.8, "Metal M2 Pro": 10.0},
+                  32: {"Metal M2 Pro": 10.8}, 80: {"WebGPU M3 Pro": 22.0, "Metal M2 Pro": 23.8}}
+
+
+def latency_table(model, cfg, reps=50):
+    """Median latency of one B=1 forward at each published T: host token ids
+    in, host f32 logits out (copies included), and device-resident."""
+    from textsift_amd import synth
+    rows = ["| T | host in/out ms (median) | device-resident ms (median) | reference (other hardware) |",
+            "|---|---|---|---|"]
+    for T in sorted(REF_LATENCY_MS):
+        ids = synth.token_ids(7 + T, T, cfg.vocab_size)
+        mask = np.ones(T, np.uint8)
+        for _ in range(5):
+            model.forward(ids, mask, 1, T)
+        host = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            model.forward(ids, mask, 1, T)
+            host.append((time.perf_counter() - t0) * 1000.0)
+        be = model.backend
+        ib, lb = be.buffer(ids), be.buffer(nbytes=T * cfg.num_classes * 4)
+        dev = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            model.forward_device(ib, None, 1, T, lb)
+            dev.append((time.perf_counter() - t0) * 1000.0)
+        ib.release()
+        lb.release()
+        ref = ", ".join(f"{k} {v} ms" for k, v in REF_LATENCY_MS[T].items())
+        rows.append(f"| {T} | {np.median(host):.3f} | {np.median(dev):.3f} | {ref} |")
+    return "\n".join(rows)
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -289,6 +326,8 @@ def main():
                     help="print a table of each forward GEMM next to a dense fp16 torch.matmul (hipBLASLt) of "
                          "the same M x N x K, then exit")
     ap.add_argument("--blas-torch", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--latency", action="store_true",
+                    help="single-sequence forward latency at the token counts the reference publishes, then exit")
     args = ap.parse_args()
 
     if args.blas_torch:  # the torch half of --blas-reference, in a process of its own
@@ -334,6 +373,10 @@ def main():
     model.finalize()
     ids_buf = be.buffer(ids)
     logits_buf = be.buffer(nbytes=M * cfg.num_classes * 4)
+
+    if args.latency:
+        print(latency_table(model, cfg))
+        return
 
     for _ in range(args.warmup):
         model.forward_device(ids_buf, None, B, T, logits_buf)
