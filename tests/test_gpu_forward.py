@@ -42,7 +42,9 @@ def test_forward_contract_errors(small):
         fresh.forward(np.zeros(4, np.int32), np.ones(4, np.uint8))
 
 
-@pytest.mark.parametrize("T,masked", [(200, False), (300, True), (5, False)])
+# (T = 5 and 40 run the expert GEMMs on 16-token tiles; all run the dense
+# GEMMs on the all-K 16-token tile)
+@pytest.mark.parametrize("T,masked", [(200, False), (300, True), (5, False), (40, True)])
 def test_small_forward_vs_oracle(small, T, masked):
     w, be = small
     ids = synth.token_ids(800 + T, T, V)

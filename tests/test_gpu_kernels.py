@@ -192,7 +192,11 @@ def folded_weights(w, N, K):
                                                 (1, 33, 640, None, 64, 1),      # classifier shape
                                                 (300, 640, 896, 8, 64, 5),      # O-projection K
                                                 (129, 1152, 640, None, 128, 4),  # fused QKV N
-                                                (200, 128, 640, 8, 128, 2)])    # router N
+                                                (200, 128, 640, 8, 128, 2),     # router N
+                                                (37, 96, 640, None, 16, 1),     # all-K 16-token tile
+                                                (1, 33, 640, None, 16, 1),
+                                                (300, 640, 896, 8, 16, 1),
+                                                (64, 128, 640, 8, 16, 2)])
 def test_matmul_w4_vs_oracle(be, T, N, K, zp, tile_t, wf):
     """The scale-folded GEMM of the fp16 forward path: against the oracle
     (exact weights, per-block f32 scaling) within the fp16 bar, and against
@@ -212,14 +216,15 @@ def test_matmul_w4_vs_oracle(be, T, N, K, zp, tile_t, wf):
     assert np.all(np.abs(out - exact) <= bound)
 
 
-def test_matmul_w4_fp16_out(be):
+@pytest.mark.parametrize("tile_t,wf", [(64, 5), (16, 1)])
+def test_matmul_w4_fp16_out(be, tile_t, wf):
     T, N, K = 70, 640, 640
     w = synth.qweight(77, N, K, zp=8)
     x = synth.to_fp16_bits(synth.normal(78, T * K)).reshape(T, K)
     o32 = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 4,
-              u32s(T, N, K, 1, 64, 5)).view(np.float32)
+              u32s(T, N, K, 1, tile_t, wf)).view(np.float32)
     o16 = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 2,
-              u32s(T, N, K, 0, 64, 5)).view(np.uint16)
+              u32s(T, N, K, 0, tile_t, wf)).view(np.uint16)
     # fp16 epilogue = the f32 result rounded as zig/math.zig:54-82 rounds
     assert np.array_equal(o16, oracle.f32_to_fp16(o32))
 
@@ -397,7 +402,8 @@ def test_router_topk_fixture(be, fixture):
         b.release()
 
 
-@pytest.mark.parametrize("T,E,tile", [(2048, 128, 64), (1, 128, 64), (32768, 128, 128), (1000, 8, 128)])
+@pytest.mark.parametrize("T,E,tile", [(2048, 128, 64), (1, 128, 64), (32768, 128, 128), (1000, 8, 128),
+                                      (300, 128, 16)])
 def test_moe_route_permutation_bit_exact(be, T, E, tile):
     K = 4
     rng = np.random.default_rng(T + E)

@@ -209,14 +209,28 @@ struct Scr {
   void* plan;
 };
 
-int tile_for(int M, int K, int E) { return (M * K / E >= 256) ? 128 : 64; }
+// The 16-token GEMM tile loads all of K (640 or 896) at once: a workgroup
+// waits on memory once instead of once per 128-wide K chunk, which is what
+// a GEMM of a few workgroups costs. fp16 numerics only.
+constexpr int SMALL_M = 512;            // dense GEMMs: rows up to this
+constexpr int SMALL_PER_EXPERT = 16;    // expert GEMMs: mean rows per expert below this
+bool small_k(size_t K) { return K == 640 || K == 896; }
+
+// Expert tile rows for the grouped GEMMs, from the mean rows per expert:
+// 128 from 256 on, 64 below, 16 (the all-K tile) below SMALL_PER_EXPERT.
+int tile_for(const pfhip_model_config& c, int M) {
+  const int per_expert = M * (int)c.topk / (int)c.experts;
+  if (per_expert >= 256) return 128;
+  const bool small = c.precision == PFHIP_PRECISION_FP16 && small_k(c.hidden) && small_k(c.dff);
+  return small && per_expert < SMALL_PER_EXPERT ? 16 : 64;
+}
 
 size_t scratch_layout(const pfhip_model_config& c, int M, Scr* s, void* base) {
   const size_t D = c.hidden, E = c.experts, K = c.topk, F = c.dff, C = c.classes;
   const size_t NQKV = (size_t)(c.heads + 2 * c.kv_heads) * c.head_dim;
   const size_t HQ = (size_t)c.heads * c.head_dim;
   const size_t S = (size_t)M * K;
-  const int tt = tile_for(M, (int)K, (int)E);
+  const int tt = tile_for(c, M);
   size_t off = 0;
   char* p = static_cast<char*>(base);
   auto take = [&](size_t bytes) -> void* {
@@ -267,7 +281,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   const int D = (int)c.hidden, E = (int)c.experts, K = (int)c.topk, F = (int)c.dff, C = (int)c.classes;
   const int Hq = (int)c.heads, Hkv = (int)c.kv_heads, hd = (int)c.head_dim;
   const int NQKV = (Hq + 2 * Hkv) * hd;
-  const int tt = tile_for(M, K, E);
+  const int tt = tile_for(c, M);
 
   // scratch
   if (M > m->cap_tokens) {
@@ -316,7 +330,9 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
 
   const bool f16 = c.precision == PFHIP_PRECISION_FP16;
   // GEMM tiles of the fp16 path: (tokens, 16-row fragments per wave)
-  const int gw_t = tt, gw_f = tt == 128 ? 4 : 5;
+  const int gw_t = tt, gw_f = tt == 128 ? 4 : (tt == 64 ? 5 : 1);
+  // dense GEMMs of at most SMALL_M rows take the all-K 16-token tile
+  auto small_dense = [&](int k) { return M <= SMALL_M && small_k((size_t)k); };
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
@@ -336,7 +352,8 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       a.seq_len = T; a.rope_cols = (Hq + Hkv) * hd;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.qkv4.w); a.wsz = L.qkv4.sz;
-        gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, 128, 4, "gemm_qkv_rope");
+        const bool sm = small_dense(D);
+        gemm_w4(b, a, XKind::F16, Epi::ROPE_F16, false, sm ? 16 : 128, sm ? 1 : 4, "gemm_qkv_rope");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::ROPE_F16, false, 128, "gemm_qkv_rope");
       }
@@ -368,7 +385,8 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (D == 640 && (Hq * hd == 640 || Hq * hd == 896) && M >= 16384) {
           gemm_w4_add_rmsnorm(b, a, h, L.ln_post, s.h2, s.xn_hi, c.eps);
         } else {
-          gemm_w4(b, a, XKind::F16, Epi::F16, false, 128, 4, "gemm_o");
+          const bool sm = small_dense(Hq * hd);
+          gemm_w4(b, a, XKind::F16, Epi::F16, false, sm ? 16 : 128, sm ? 1 : 4, "gemm_o");
           add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
         }
       } else {
@@ -391,7 +409,8 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
         }
-        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, 128, 2, "gemm_router");
+        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D) ? 16 : 128, 2,
+                "gemm_router");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
       }
@@ -446,7 +465,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
     if (f16) {
       a.w = reinterpret_cast<const uint8_t*>(m->score4.w); a.wsz = m->score4.sz;
-      gemm_w4(b, a, XKind::F16, Epi::F16, false, 64, 1, "gemm_classifier");
+      gemm_w4(b, a, XKind::F16, Epi::F16, false, small_dense(D) ? 16 : 64, 1, "gemm_classifier");
     } else {
       gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
     }

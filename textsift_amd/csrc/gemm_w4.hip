@@ -96,7 +96,6 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 template <int WF, int BT, Epi EPI, int NW = 4>
 struct StagedOut {
   static constexpr bool F32OUT = EPI == Epi::F32 || EPI == Epi::F32_TOPK;
-  static constexpr bool OK = F32OUT || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16;
   static constexpr int ESZ = F32OUT ? 4 : 2;
   static constexpr int CF = EPI == Epi::SWIGLU_F16 ? 8 : 16;
   static constexpr int FB = CF * ESZ;
@@ -107,13 +106,19 @@ struct StagedOut {
   static constexpr int UP = PRB / 16;
   static constexpr int SWM = UP % 16 == 0 ? 15 : (UP % 8 == 0 ? 7 : (UP % 4 == 0 ? 3 : 0));
   static constexpr size_t LDS = (size_t)BT * PRB;
-  static_assert(BT * UP % (64 * NW) == 0, "staged stores: whole rounds of one unit per thread");
+  // (small tiles store directly: fewer units than threads)
+  static constexpr bool OK = (F32OUT || EPI == Epi::F16 || EPI == Epi::ROPE_F16 || EPI == Epi::SWIGLU_F16) &&
+                             BT * UP % (64 * NW) == 0;
 };
 
 // NW waves per workgroup (4: two workgroups per CU; 8 measured on a
 // 256-token tile: each dequantised fragment feeds twice the MFMAs, but the
 // doubled activation reads from LDS cancel it: gate_up -2 %, down +10 %)
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4>
+// CT > 0 (small tiles): K / 128 at compile time; every chunk's activations
+// and weights are loaded at once, so a workgroup waits for memory once
+// instead of once per chunk (the latency that dominates when a GEMM is a few
+// workgroups).
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
@@ -235,11 +240,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
-  auto compute = [&](int buf) {
+  auto compute = [&](int buf, const u4_t (&wr)[WF], const uint32_t (&szc)[WF]) {
     h2_t off[WF], sc[WF];
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
-      const h2_t pr = __builtin_bit_cast(h2_t, sz[f]);
+      const h2_t pr = __builtin_bit_cast(h2_t, szc[f]);
       off[f] = h2_t{pr.x, pr.x};
       sc[f] = h2_t{pr.y, pr.y};
     }
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
 #pragma unroll
-      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wraw[f][j], off[f], sc[f]);
+      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wr[f][j], off[f], sc[f]);
       const int unit = ((4 * lg + j) ^ l16) << 3;
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) {
@@ -265,22 +270,34 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     }
   };
 
-  load_x(0, 0);
-  load_w(0, wraw, sz);
-  for (int c = 0; c + 1 < C; ++c) {
+  [[maybe_unused]] u4_t wall[CT > 0 ? CT : 1][WF];
+  [[maybe_unused]] uint32_t szall[CT > 0 ? CT : 1][WF];
+  if constexpr (CT > 0) {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      load_x(c, c);
+      load_w(c, wall[c], szall[c]);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    load_x(c + 1, (c & 1) ^ 1);
-    load_w(c + 1, wnext, sznext);
-    compute(c & 1);
+  } else {
+    load_x(0, 0);
+    load_w(0, wraw, sz);
+    for (int c = 0; c + 1 < C; ++c) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      load_x(c + 1, (c & 1) ^ 1);
+      load_w(c + 1, wnext, sznext);
+      compute(c & 1, wraw, sz);
 #pragma unroll
-    for (int f = 0; f < WF; ++f) {
-      wraw[f] = wnext[f];
-      sz[f] = sznext[f];
+      for (int f = 0; f < WF; ++f) {
+        wraw[f] = wnext[f];
+        sz[f] = sznext[f];
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
 
   // ---- RoPE operands, loaded before the last chunk's MFMAs so that their
   // latency overlaps them.
@@ -289,22 +306,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   // not use, their eight 16-byte units XOR-swizzled by (row & 7). Row r of
   // the tile is at position (row0 + r) mod seq_len. One wave instruction
   // fills 8 rows.
+  // (with CT > 0 every chunk buffer is in use and the table goes after them)
+  const int tbuf = CT > 0 ? CT : (C & 1);
   if constexpr (EPI == Epi::ROPE_F16) {
-    static_assert(BT % (8 * NW) == 0, "RoPE table staging: whole rounds of 8 rows per wave");
+    static_assert(BT % 8 == 0, "RoPE table staging: whole 8-row copies");
     const int p0 = (int)((uint32_t)row0 % (uint32_t)p.seq_len);
-    _Float16* tb = xs_lds + (C & 1) * XS * PLANE;
-#pragma unroll
-    for (int m = 0; m < BT / (8 * NW); ++m) {
-      const int r = (m * NW + wave) * 8 + (lane >> 3);
+    _Float16* tb = xs_lds + tbuf * XS * PLANE;
+    for (int u8 = wave; u8 < BT / 8; u8 += NW) {  // wave-uniform
+      const int r = u8 * 8 + (lane >> 3);
       int q = p0 + r;
       if (p.seq_len >= BT) q = q >= p.seq_len ? q - p.seq_len : q;
       else q %= p.seq_len;
       const int u = (lane & 7) ^ (r & 7);  // this lane's unit lands at position lane & 7 of row r
-      copy16_to_lds(p.rope_pairs + (size_t)q * 64 + u * 8, (lds_ptr_t)(tb + (m * NW + wave) * 512));
+      copy16_to_lds(p.rope_pairs + (size_t)q * 64 + u * 8, (lds_ptr_t)(tb + u8 * 512));
     }
   }
 
-  compute((C - 1) & 1);
+  if constexpr (CT > 0) {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) compute(c, wall[c], szall[c]);
+  } else {
+    compute((C - 1) & 1, wraw, sz);
+  }
   if constexpr (EPI == Epi::ROPE_F16) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -331,7 +354,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
           if constexpr (EPI == Epi::ROPE_F16) {
             if (rope) {
               const int row = 16 * tj + l16;
-              ow[f][tj] = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, row, pidx));
+              ow[f][tj] = rope_f16x4_native(v, rope_entry(xs_lds + tbuf * XS * PLANE, row, pidx));
             } else {
               ow[f][tj] = to_f16x4_native(v);
             }
@@ -373,13 +396,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
               *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
       }
     }
-    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 == 64 * NW) {
+    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 <= 64 * NW) {
       // Router top-4 of every row from the staged tile (all N == 128 logits
       // of BT rows are in LDS): two threads per row each take the top-4 of
       // one half by the reference's insertion rule, then the halves merge by
       // (value descending, index ascending), which is what the insertion
       // over the whole row yields without NaNs; a row with a NaN replays the
-      // sequential insertion over all 128 logits.
+      // sequential insertion over all 128 logits. (Threads past 2 BT idle;
+      // both threads of a pair are always active together.)
+      if (tid >= 2 * BT) return;
       const int row = tid >> 1, half = tid & 1;
       const char* rb = ob + row * SO::PRB;
       auto at = [&](int c) -> float {
@@ -460,7 +485,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       if constexpr (EPI == Epi::ROPE_F16) {
         u2_t hv;
         if (rope) {
-          hv = rope_f16x4_native(v, rope_entry(xs_lds + (C & 1) * XS * PLANE, lt, pidx));
+          hv = rope_f16x4_native(v, rope_entry(xs_lds + tbuf * XS * PLANE, lt, pidx));
         } else {
           hv = to_f16x4_native(v);
         }
@@ -477,7 +502,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 }
 
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4>
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0>
 void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   constexpr int BN = NW * WF * 16;
   const int n_tiles = (a.N + BN - 1) / BN;
@@ -485,42 +510,63 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   const long grid = (long)n_tiles * t_tiles;
   if (grid == 0) return;
   PF_CHECK(grid < (1L << 31), "gemm_w4: grid too large");
-  const size_t lds = std::max((size_t)2 * XS * BT * KC * sizeof(uint16_t),
+  PF_CHECK(CT == 0 || a.K == CT * KC, "gemm_w4: K does not match the tile's compile-time chunk count");
+  // activation buffers: two (double buffering) or all CT chunks, plus the
+  // RoPE table's plane when every chunk buffer is taken
+  constexpr int NBUF = CT > 0 ? CT + (EPI == Epi::ROPE_F16 ? 1 : 0) : 2;
+  const size_t lds = std::max((size_t)NBUF * XS * BT * KC * sizeof(uint16_t),
                               StagedOut<WF, BT, EPI, NW>::OK ? StagedOut<WF, BT, EPI, NW>::LDS : (size_t)0);
   static bool attr_set = false;  // per template instance
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW>),
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
   ProfScope ps(b, name);
-  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW>), dim3((unsigned)grid), dim3(64 * NW), lds, b->stream,
-                     a);
+  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT>), dim3((unsigned)grid), dim3(64 * NW), lds,
+                     b->stream, a);
   PF_HIP(hipGetLastError());
 }
 
-template <int WF, int BT, int XS, bool GROUPED, int NW>
+template <int WF, int BT, int XS, bool GROUPED, int NW, int CT = 0>
 void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name) {
+  // the small tile (CT > 0) is built with one fragment per wave for every
+  // epilogue and with two for the router's (N = 128 in one workgroup)
+  constexpr bool ALL = CT == 0 || WF == 1;
   switch (epi) {
-    case Epi::F16: return launch<WF, BT, XS, Epi::F16, GROUPED, NW>(b, a, name);
-    case Epi::F32: return launch<WF, BT, XS, Epi::F32, GROUPED, NW>(b, a, name);
+    case Epi::F16:
+      if constexpr (ALL) return launch<WF, BT, XS, Epi::F16, GROUPED, NW, CT>(b, a, name);
+      break;
+    case Epi::F32: return launch<WF, BT, XS, Epi::F32, GROUPED, NW, CT>(b, a, name);
     case Epi::ROPE_F16:
-      if constexpr (NW == 4) return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED, NW>(b, a, name);
+      if constexpr (NW == 4 && ALL && !GROUPED) return launch<WF, BT, XS, Epi::ROPE_F16, GROUPED, NW, CT>(b, a, name);
       break;
     case Epi::SWIGLU_SPLIT: break;
-    case Epi::SWIGLU_F16: return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED, NW>(b, a, name);
+    case Epi::SWIGLU_F16:
+      if constexpr (ALL) return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED, NW, CT>(b, a, name);
+      break;
     case Epi::F32_TOPK:
-      if constexpr (WF == 2 && BT == 128 && !GROUPED && NW == 4)
-        return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW>(b, a, name);
+      if constexpr (WF == 2 && (BT == 128 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4)
+        return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT>(b, a, name);
       break;
   }
   throw Error("gemm_w4: unsupported epilogue for this tile");
 }
 
-template <int WF, int BT, int NW = 4>
+template <int WF, int BT, int NW = 4, int CT = 0>
 void dispatch_grouped(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped, const char* name) {
-  if (grouped) dispatch_epi<WF, BT, 1, true, NW>(b, a, epi, name);
-  else dispatch_epi<WF, BT, 1, false, NW>(b, a, epi, name);
+  if (grouped) dispatch_epi<WF, BT, 1, true, NW, CT>(b, a, epi, name);
+  else dispatch_epi<WF, BT, 1, false, NW, CT>(b, a, epi, name);
+}
+
+// 16-token tile with all of K loaded at once: K = 640 or 896 (5 or 7 chunks)
+template <int WF>
+void dispatch_small(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped, const char* name) {
+  switch (a.K / KC) {
+    case 5: return dispatch_grouped<WF, 16, 4, 5>(b, a, epi, grouped, name);
+    case 7: return dispatch_grouped<WF, 16, 4, 7>(b, a, epi, grouped, name);
+    default: throw Error("gemm_w4: the 16-token tile is built for K = 640 and 896");
+  }
 }
 
 // ---------------------------------------------------------------- weight prep
@@ -593,13 +639,16 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   }
   PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
   if (epi == Epi::F32_TOPK)
-    PF_CHECK(!grouped && tile_t == 128 && wf == 2 && a.N == 128 && a.topk_k == 4 && a.topk_idx && a.topk_w &&
-                 g.out_staged,
-             "gemm_w4: the top-k epilogue needs N == 128, K == 4, the 128 x 128 tile and 16-byte aligned f32 rows");
+    PF_CHECK(!grouped && (tile_t == 128 || tile_t == 16) && wf == 2 && a.N == 128 && a.topk_k == 4 && a.topk_idx &&
+                 a.topk_w && g.out_staged,
+             "gemm_w4: the top-k epilogue needs N == 128, K == 4, a 128- or 16-token tile of 128 columns and "
+             "16-byte aligned f32 rows");
   if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, g, epi, grouped, prof_name);
+  if (tile_t == 16 && wf == 1) return dispatch_small<1>(b, g, epi, grouped, prof_name);
+  if (tile_t == 16 && wf == 2) return dispatch_small<2>(b, g, epi, grouped, prof_name);
   throw Error("gemm_w4: unsupported (tile_t, wf) = (" + std::to_string(tile_t) + ", " + std::to_string(wf) + ")");
 }
 

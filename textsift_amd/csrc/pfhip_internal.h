@@ -132,7 +132,9 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
                const char* prof_name);
 
 // Scale-folded int4 GEMM (gemm_w4.hip): weights prepared by w4_prepare;
-// K % 128 == 0. tile_t x wf selects the tile (BT tokens x 64*wf rows).
+// K % 128 == 0. tile_t x wf selects the tile (BT tokens x 64*wf rows):
+// (128, 4), (128, 2), (64, 5), (64, 1), and the small-M tiles (16, 1) and
+// (16, 2) that load all of K (640 or 896) at once.
 void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t, int wf,
              const char* prof_name);
 // O projection (gemm_w4 weights, N == 640, bias folded as in gemm_w4) with the

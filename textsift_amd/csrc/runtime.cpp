@@ -340,7 +340,7 @@ static std::vector<KernelEntry>& registry() {
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), K = (int)pu(p, 1), E = (int)pu(p, 2), tt = (int)pu(p, 3);
-                 PF_CHECK(tt == 64 || tt == 128, "moe_route: tile_t must be 64 or 128");
+                 PF_CHECK(tt == 16 || tt == 64 || tt == 128, "moe_route: tile_t must be 16, 64 or 128");
                  need(bs, 0, (size_t)T * K * 4, "moe_route");
                  need(bs, 1, (size_t)(E + 1) * 4, "moe_route");
                  need(bs, 2, (size_t)T * K * 4, "moe_route");
