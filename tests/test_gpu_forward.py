@@ -72,6 +72,20 @@ def test_batched_forward_equals_per_sequence(small):
         assert np.array_equal(got[b], one)
 
 
+def test_forward_is_deterministic(small):
+    """The same sequence twice, with forwards of other sizes (other GEMM
+    tiles, expert tile lists and scratch layouts) in between: bit-identical
+    logits."""
+    w, be = small
+    T = 700
+    ids = synth.token_ids(950, T, V)
+    first = be.forward(ids, np.ones(T, np.uint8)).as_matrix().copy()
+    for t in (5, 40, 300, 2100):
+        be.forward(synth.token_ids(951 + t, t, V), np.ones(t, np.uint8))
+    again = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
+    assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+
+
 def test_per_layer_taps_vs_oracle_block(small):
     w, be = small
     T = 256

@@ -79,7 +79,6 @@ struct pfhip_model {
   // per-forward scratch
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
-  int cap_tokens = 0;
   // RoPE tables for one sequence length
   int rope_T = 0;
   float* rope_cos = nullptr;  // fp16 table entries, widened as the reference widens them
@@ -212,8 +211,8 @@ struct Scr {
 // The 16-token GEMM tile loads all of K (640 or 896) at once: a workgroup
 // waits on memory once instead of once per 128-wide K chunk, which is what
 // a GEMM of a few workgroups costs. fp16 numerics only.
-constexpr int SMALL_M = 512;            // dense GEMMs: rows up to this
-constexpr int SMALL_PER_EXPERT = 16;    // expert GEMMs: mean rows per expert below this
+constexpr int SMALL_M = 2048;           // dense GEMMs: rows up to this
+constexpr int SMALL_PER_EXPERT = 32;    // expert GEMMs: mean rows per expert below this
 bool small_k(size_t K) { return K == 640 || K == 896; }
 
 // Expert tile rows for the grouped GEMMs, from the mean rows per expert:
@@ -283,9 +282,10 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   const int NQKV = (Hq + 2 * Hkv) * hd;
   const int tt = tile_for(c, M);
 
-  // scratch
-  if (M > m->cap_tokens) {
-    const size_t bytes = scratch_layout(c, M, nullptr, nullptr);
+  // scratch (the layout's size is not monotonic in M: the expert tile list
+  // of a smaller M on a smaller tile can be longer)
+  const size_t bytes = scratch_layout(c, M, nullptr, nullptr);
+  if (bytes > m->scratch_bytes) {
     if (m->scratch) {
       PF_HIP(hipStreamSynchronize(b->stream));
       PF_HIP(hipFree(m->scratch));
@@ -293,7 +293,6 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     }
     PF_HIP(hipMalloc(&m->scratch, bytes));
     m->scratch_bytes = bytes;
-    m->cap_tokens = M;
   }
   Scr s;
   scratch_layout(c, M, &s, m->scratch);
@@ -331,8 +330,9 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   const bool f16 = c.precision == PFHIP_PRECISION_FP16;
   // GEMM tiles of the fp16 path: (tokens, 16-row fragments per wave)
   const int gw_t = tt, gw_f = tt == 128 ? 4 : (tt == 64 ? 5 : 1);
-  // dense GEMMs of at most SMALL_M rows take the all-K 16-token tile
-  auto small_dense = [&](int k) { return M <= SMALL_M && small_k((size_t)k); };
+  // dense GEMMs of at most SMALL_M rows (O and the classifier 2x, the
+  // router 8x: measured crossovers) take the all-K 16-token tile
+  auto small_dense = [&](int k, int limit = SMALL_M) { return M <= limit && small_k((size_t)k); };
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
@@ -385,7 +385,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (D == 640 && (Hq * hd == 640 || Hq * hd == 896) && M >= 16384) {
           gemm_w4_add_rmsnorm(b, a, h, L.ln_post, s.h2, s.xn_hi, c.eps);
         } else {
-          const bool sm = small_dense(Hq * hd);
+          const bool sm = small_dense(Hq * hd, 2 * SMALL_M);
           gemm_w4(b, a, XKind::F16, Epi::F16, false, sm ? 16 : 128, sm ? 1 : 4, "gemm_o");
           add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
         }
@@ -409,7 +409,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
         }
-        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D) ? 16 : 128, 2,
+        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D, 8 * SMALL_M) ? 16 : 128, 2,
                 "gemm_router");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
@@ -465,7 +465,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
     if (f16) {
       a.w = reinterpret_cast<const uint8_t*>(m->score4.w); a.wsz = m->score4.sz;
-      gemm_w4(b, a, XKind::F16, Epi::F16, false, small_dense(D) ? 16 : 64, 1, "gemm_classifier");
+      gemm_w4(b, a, XKind::F16, Epi::F16, false, small_dense(D, 2 * SMALL_M) ? 16 : 64, 1, "gemm_classifier");
     } else {
       gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
     }

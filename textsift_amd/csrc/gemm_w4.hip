@@ -396,72 +396,86 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
               *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
       }
     }
-    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128 && BT * 2 <= 64 * NW) {
+    if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128) {
       // Router top-4 of every row from the staged tile (all N == 128 logits
-      // of BT rows are in LDS): two threads per row each take the top-4 of
-      // one half by the reference's insertion rule, then the halves merge by
-      // (value descending, index ascending), which is what the insertion
-      // over the whole row yields without NaNs; a row with a NaN replays the
-      // sequential insertion over all 128 logits. (Threads past 2 BT idle;
-      // both threads of a pair are always active together.)
-      if (tid >= 2 * BT) return;
-      const int row = tid >> 1, half = tid & 1;
+      // of BT rows are in LDS). TPR threads share a row, each taking the
+      // top-4 of SEG consecutive logits by the reference's insertion rule;
+      // the lists then merge pairwise by (value descending, index
+      // ascending), the lower segment winning ties, which is what the
+      // insertion over the whole row yields without NaNs. A row with a NaN
+      // replays the sequential insertion over all 128 logits.
+      constexpr int TPR = 64 * NW / BT, SEG = 128 / TPR;
+      static_assert(TPR >= 2 && TPR <= 32 && (TPR & (TPR - 1)) == 0, "top-k: 2..32 threads per row");
+      const int row = tid / TPR, part = tid % TPR;
       const char* rb = ob + row * SO::PRB;
       auto at = [&](int c) -> float {
         return *reinterpret_cast<const float*>(rb + (((c >> 2) ^ (row & SO::SWM)) << 4) + (c & 3) * 4);
       };
       float V[4];
       int I[4];
-      topk_insertion<4>([&](int c) { return at(64 * half + c); }, 64, V, I);
+      topk_insertion<4>([&](int c) { return at(SEG * part + c); }, SEG, V, I);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) I[k] += SEG * part;
       bool nan = false;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const f4_t q = *reinterpret_cast<const f4_t*>(rb + (((16 * half + u) ^ (row & SO::SWM)) << 4));
+      for (int u = 0; u < SEG / 4; ++u) {
+        const f4_t q = *reinterpret_cast<const f4_t*>(rb + ((((SEG / 4) * part + u) ^ (row & SO::SWM)) << 4));
         nan = nan | (q[0] != q[0]) | (q[1] != q[1]) | (q[2] != q[2]) | (q[3] != q[3]);
       }
-      nan = nan | (__shfl_xor((int)nan, 1, 64) != 0);
-      float BV[4];
-      int BI[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        BV[k] = __shfl_xor(V[k], 1, 64);
-        BI[k] = __shfl_xor(I[k], 1, 64) + 64;
-      }
-      if (half == 0 && row < rows) {
-        float RV[4];
-        int RI[4];
-        if (nan) {
-          topk_insertion<4>(at, 128, RV, RI);
-        } else {
-          // rank of each candidate among the 8; the first half (lower ids) wins ties
+      for (int sft = 1; sft < TPR; sft <<= 1) {
+        nan = nan | (__shfl_xor((int)nan, sft, 64) != 0);
+        float OV[4];
+        int OI[4];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            RV[k] = 0.0f;
-            RI[k] = 0;
+        for (int k = 0; k < 4; ++k) {
+          OV[k] = __shfl_xor(V[k], sft, 64);
+          OI[k] = __shfl_xor(I[k], sft, 64);
+        }
+        // A: the lower segment's list, B: the upper one's
+        const bool lower = (part & sft) == 0;
+        float AV[4], BV[4], RV[4];
+        int AI[4], BI[4], RI[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          AV[k] = lower ? V[k] : OV[k];
+          AI[k] = lower ? I[k] : OI[k];
+          BV[k] = lower ? OV[k] : V[k];
+          BI[k] = lower ? OI[k] : I[k];
+          RV[k] = 0.0f;
+          RI[k] = 0;
+        }
+        // rank of each candidate among the 8
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          int ra = i, rbk = i;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            ra += BV[j] > AV[i];
+            rbk += AV[j] >= BV[i];
           }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            int ra = i, rbk = i;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              ra += BV[j] > V[i];
-              rbk += V[j] >= BV[i];
+          for (int k = 0; k < 4; ++k) {
+            if (ra == k) {
+              RV[k] = AV[i];
+              RI[k] = AI[i];
             }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              if (ra == k) {
-                RV[k] = V[i];
-                RI[k] = I[i];
-              }
-              if (rbk == k) {
-                RV[k] = BV[i];
-                RI[k] = BI[i];
-              }
+            if (rbk == k) {
+              RV[k] = BV[i];
+              RI[k] = BI[i];
             }
           }
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          V[k] = RV[k];
+          I[k] = RI[k];
+        }
+      }
+      if (part == 0 && row < rows) {
+        if (nan) topk_insertion<4>(at, 128, V, I);
         const size_t t = (size_t)(row0 + row);
-        topk_write<4>(RV, RI, p.topk_wscale, p.topk_idx + t * 4, p.topk_w + t * 4);
+        topk_write<4>(V, I, p.topk_wscale, p.topk_idx + t * 4, p.topk_w + t * 4);
       }
     }
     return;
