@@ -47,8 +47,11 @@ KERNEL_LABELS = [
     ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false")),
     ("gemm_o_add_rmsnorm", ("k_gemm_w4_rownorm",)),
     ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false")),
-    ("gemm_router", ("k_gemm_w4<2, 128", "(pf::Epi)5, false")),
+    ("gemm_o", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 7>")),      # all-K small tile, K = 896
+    ("gemm_router", ("k_gemm_w4<2, ", "(pf::Epi)5, false")),
+    ("gemm_router", ("k_gemm_w4<2, ", "(pf::Epi)1, false")),
     ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false")),
+    ("gemm_classifier", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 5>")),  # all-K small tile, K = 640
     ("banded_attention", ("k_banded_attention",)),
     ("moe_combine_norm", ("k_moe_combine",)),
     ("add_rmsnorm_f16", ("k_add_rms_norm",)),
@@ -60,6 +63,9 @@ KERNEL_LABELS = [
     ("rms_norm", ("k_rms_norm",)),
     ("copy", ("k_copy16",)),
 ]
+
+
+LABELS = list(dict.fromkeys(lab for lab, _ in KERNEL_LABELS))  # unique, in order
 
 
 def label_of(symbol):
@@ -112,7 +118,7 @@ def traffic_report(fetch_csv, write_csv, copy_mb):
     lines = ["| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/launch |",
              "|---|---|---|---|---|"]
     summary = {}
-    for lab, _ in KERNEL_LABELS:
+    for lab in LABELS:
         if lab == "copy" or lab not in fl or lab not in wl:
             continue
         f = sum(fl[lab]) / len(fl[lab])
@@ -149,7 +155,7 @@ def sq_report(p1_csv, p2_csv, cus=256, ses=32):
                     per.setdefault(lab, {}).setdefault(cn, {})[(path, d)] = v
     lines = ["| kernel | waves | VALU / wave | MFMA / wave | SALU / wave | LDS / wave | LDS conflict cycles / LDS instr | "
              "MFMA busy | wave time waiting on dependencies |", "|---|---|---|---|---|---|---|---|---|"]
-    for lab, _ in KERNEL_LABELS:
+    for lab in LABELS:
         if lab not in per or any(n not in per[lab] for n in names):
             continue
         a = {n: sum(per[lab][n].values()) / len(per[lab][n]) for n in names}

@@ -216,6 +216,22 @@ def test_matmul_w4_vs_oracle(be, T, N, K, zp, tile_t, wf):
     assert np.all(np.abs(out - exact) <= bound)
 
 
+@pytest.mark.parametrize("N,K", [(1152, 640), (640, 896), (128, 640)])
+def test_matmul_w4_tiles_bit_identical(be, N, K):
+    """Every tile (the double-buffered ones and the all-K 16-token one) runs
+    the same MFMA fragments in the same K order: identical f32 outputs."""
+    T = 300
+    w = synth.qweight(500 + N, N, K, zp=8)
+    x = synth.to_fp16_bits(synth.normal(501 + K, T * K)).reshape(T, K)
+    outs = {}
+    for tile_t, wf in [(128, 4), (128, 2), (64, 5), (64, 1), (16, 1), (16, 2)]:
+        outs[(tile_t, wf)] = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 4,
+                                 u32s(T, N, K, 1, tile_t, wf)).view(np.uint32)
+    base = outs[(128, 4)]
+    for k, o in outs.items():
+        assert np.array_equal(o, base), f"tile {k} differs from (128, 4)"
+
+
 @pytest.mark.parametrize("tile_t,wf", [(64, 5), (16, 1)])
 def test_matmul_w4_fp16_out(be, tile_t, wf):
     T, N, K = 70, 640, 640
