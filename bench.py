@@ -56,6 +56,7 @@ KERNEL_LABELS = [
     ("moe_combine_norm", ("k_moe_combine",)),
     ("add_rmsnorm_f16", ("k_add_rms_norm",)),
     ("router_topk", ("k_router_topk",)),
+    ("moe_route", ("k_moe_route_small",)),
     ("moe_count", ("k_moe_count",)),
     ("moe_scan", ("k_moe_scan",)),
     ("moe_scatter", ("k_moe_scatter",)),

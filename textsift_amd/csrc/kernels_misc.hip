@@ -475,6 +475,79 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
   }
 }
 
+// All three steps in one workgroup when every token fits one counting block
+// (T <= RBLK): the bitmap, per-expert counts, the exclusive scans over
+// experts (rows and tiles) and the slot assignment. Same outputs as the
+// three kernels (expert_off, slot_token, slot_of, tiles, num_tiles; counts
+// and blk_off are not written: nothing else reads them).
+__global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restrict__ idx,
+                                                          int32_t* __restrict__ expert_off,
+                                                          int32_t* __restrict__ slot_token,
+                                                          int32_t* __restrict__ slot_of, int32_t* __restrict__ tiles,
+                                                          int32_t* __restrict__ num_tiles, int T, int K, int E,
+                                                          int tile_t) {
+  __shared__ uint32_t bits[256 * (RBLK / 32)];
+  __shared__ int32_t off[256], wsum[2][RBLK / 64];
+  moe_block_bitmap(idx, bits, 0, T, K, E);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // rows c and tiles n of expert e = tid; inclusive scans within the wave
+  int c = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[tid * (RBLK / 32) + w]);
+  }
+  const int n = (c + tile_t - 1) / tile_t;
+  int ci = c, ni = n;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(ci, o, 64), bb = __shfl_up(ni, o, 64);
+    if (lane >= o) {
+      ci += a;
+      ni += bb;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][wv] = ci;
+    wsum[1][wv] = ni;
+  }
+  __syncthreads();
+  int cb = 0, nbase = 0, ct = 0, nt = 0;
+#pragma unroll
+  for (int w = 0; w < RBLK / 64; ++w) {
+    cb += w < wv ? wsum[0][w] : 0;
+    nbase += w < wv ? wsum[1][w] : 0;
+    ct += wsum[0][w];
+    nt += wsum[1][w];
+  }
+  const int base = cb + ci - c;  // exclusive prefix of rows
+  int tix = nbase + ni - n;      // exclusive prefix of tiles
+  if (tid < E) {
+    off[tid] = base;
+    expert_off[tid] = base;
+    for (int r = 0; r < c; r += tile_t, ++tix)
+      reinterpret_cast<int4*>(tiles)[tix] = int4{tid, base + r, min(tile_t, c - r), 0};
+  }
+  if (tid == 0) {
+    expert_off[E] = ct;
+    *num_tiles = nt;
+  }
+  __syncthreads();
+  if (tid >= T) return;
+  const int wl = tid >> 5;
+  const uint32_t below = (1u << (tid & 31)) - 1u;
+  for (int k = 0; k < K; ++k) {
+    const size_t i = (size_t)tid * K + k;
+    const int e = idx[i];
+    if ((unsigned)e >= (unsigned)E) continue;
+    const uint32_t* be = bits + e * (RBLK / 32);
+    int rank = __popc(be[wl] & below);
+    for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
+    const int pos = off[e] + rank;
+    slot_token[pos] = tid;
+    slot_of[i] = pos;
+  }
+}
+
 // ----------------------------------------------------------------------------
 // MoE combine (scatter_add_weighted_f32 :1027-1055 + cast_f32_to_fp16_scaled
 // :1153-1164 + add_fp16). Each token sums its K expert outputs in ascending
@@ -954,6 +1027,13 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
   PF_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= MAXK, "moe_route: need E <= 256 and K <= 8");
   if (T <= 0) return;
   const int nblk = (T + RBLK - 1) / RBLK;
+  if (nblk == 1) {
+    ProfScope ps(b, "moe_route");
+    hipLaunchKernelGGL(k_moe_route_small, dim3(1), dim3(RBLK), 0, b->stream, idx, m.expert_off, m.slot_token,
+                       m.slot_of, m.tiles, m.num_tiles, T, K, E, m.tile_t);
+    PF_HIP(hipGetLastError());
+    return;
+  }
   {
     ProfScope ps(b, "moe_count");
     hipLaunchKernelGGL(k_moe_count, dim3(nblk), dim3(256), 0, b->stream, idx, m.counts, T, K, E);
