@@ -300,7 +300,8 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 // expert, reproducing the reference's per-expert lists (for e ascending, the
 // pairs with expert e in ascending token order: browser/inference/
 // expert.ts:125-145). Deterministic: no atomics anywhere.
-constexpr int RBLK = 256;  // tokens per counting block
+constexpr int RBLK = 1024;          // tokens per counting block
+constexpr int BWS = RBLK / 32 + 1;  // bitmap words per expert in LDS (padded: rows in distinct banks)
 
 // Per-block expert bitmaps: bit t of bits[e][t / 32] is set when token t of
 // the block routes to expert e. OR is order-independent, so the bitmap (and
@@ -308,13 +309,13 @@ constexpr int RBLK = 256;  // tokens per counting block
 // outside [0, E) are ignored.
 __device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx, uint32_t* bits, int t0, int nt,
                                                  int K, int E) {
-  for (int i = threadIdx.x; i < E * (RBLK / 32); i += blockDim.x) bits[i] = 0u;
+  for (int i = threadIdx.x; i < E * BWS; i += blockDim.x) bits[i] = 0u;
   __syncthreads();
   const int tl = threadIdx.x;
   if (tl < nt)
     for (int k = 0; k < K; ++k) {
       const int e = idx[(size_t)(t0 + tl) * K + k];
-      if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * (RBLK / 32) + (tl >> 5)], 1u << (tl & 31));
+      if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * BWS + (tl >> 5)], 1u << (tl & 31));
     }
   __syncthreads();
 }
@@ -322,14 +323,14 @@ __device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx
 // counts[blk][e] = tokens of block blk routed to expert e.
 __global__ __launch_bounds__(RBLK) void k_moe_count(const int32_t* __restrict__ idx, int32_t* __restrict__ counts,
                                                     int T, int K, int E) {
-  __shared__ uint32_t bits[256 * (RBLK / 32)];
+  __shared__ uint32_t bits[256 * BWS];
   const int blk = blockIdx.x;
   const int t0 = blk * RBLK;
   moe_block_bitmap(idx, bits, t0, min(RBLK, T - t0), K, E);
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int c = 0;
 #pragma unroll
-    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[e * (RBLK / 32) + w]);
+    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[e * BWS + w]);
     counts[(size_t)blk * E + e] = c;
   }
 }
@@ -356,7 +357,17 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __rest
   const int per = (nblk + G - 1) / G;
   const int b0 = min(nblk, j * per), b1 = min(nblk, b0 + per);
   int sum = 0;
-  if (e < E) {
+  // up to 8 blocks per thread (every shape up to 8 * G counting blocks): the
+  // counts are loaded once, all in flight together, and kept for the offsets
+  constexpr int PR = 8;
+  const bool held = per <= PR;
+  int cv[PR];
+  if (held) {
+#pragma unroll
+    for (int u = 0; u < PR; ++u) cv[u] = (e < E && b0 + u < b1) ? counts[(size_t)(b0 + u) * E + e] : 0;
+#pragma unroll
+    for (int u = 0; u < PR; ++u) sum += cv[u];
+  } else if (e < E) {
     int b = b0;
     for (; b + 8 <= b1; b += 8) {  // independent loads in flight
       int c[8];
@@ -421,7 +432,15 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __rest
     const int base = tot[e];
     if (j == 0) expert_off[e] = base;
     int run = base + part[j * E2 + e];
-    int b = b0;
+    int b = held ? b1 : b0;
+    if (held) {
+#pragma unroll
+      for (int u = 0; u < PR; ++u)
+        if (b0 + u < b1) {
+          blk_off[(size_t)(b0 + u) * E + e] = run;
+          run += cv[u];
+        }
+    }
     for (; b + 8 <= b1; b += 8) {
       int c[8];
 #pragma unroll
@@ -453,7 +472,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
                                                       const int32_t* __restrict__ blk_off,
                                                       int32_t* __restrict__ slot_token, int32_t* __restrict__ slot_of,
                                                       int T, int K, int E) {
-  __shared__ uint32_t bits[256 * (RBLK / 32)];
+  __shared__ uint32_t bits[256 * BWS];
   const int blk = blockIdx.x;
   const int t0 = blk * RBLK;
   const int nt = min(RBLK, T - t0);
@@ -466,7 +485,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
     const size_t i = (size_t)(t0 + tl) * K + k;
     const int e = idx[i];
     if ((unsigned)e >= (unsigned)E) continue;
-    const uint32_t* be = bits + e * (RBLK / 32);
+    const uint32_t* be = bits + e * BWS;
     int rank = __popc(be[wl] & below);
     for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
     const int pos = blk_off[(size_t)blk * E + e] + rank;
@@ -486,7 +505,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
                                                           int32_t* __restrict__ slot_of, int32_t* __restrict__ tiles,
                                                           int32_t* __restrict__ num_tiles, int T, int K, int E,
                                                           int tile_t) {
-  __shared__ uint32_t bits[256 * (RBLK / 32)];
+  __shared__ uint32_t bits[256 * BWS];
   __shared__ int32_t off[256], wsum[2][RBLK / 64];
   moe_block_bitmap(idx, bits, 0, T, K, E);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -494,7 +513,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
   int c = 0;
   if (tid < E) {
 #pragma unroll
-    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[tid * (RBLK / 32) + w]);
+    for (int w = 0; w < RBLK / 32; ++w) c += __popc(bits[tid * BWS + w]);
   }
   const int n = (c + tile_t - 1) / tile_t;
   int ci = c, ni = n;
@@ -539,7 +558,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
     const size_t i = (size_t)tid * K + k;
     const int e = idx[i];
     if ((unsigned)e >= (unsigned)E) continue;
-    const uint32_t* be = bits + e * (RBLK / 32);
+    const uint32_t* be = bits + e * BWS;
     int rank = __popc(be[wl] & below);
     for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
     const int pos = off[e] + rank;
@@ -1036,7 +1055,7 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
   }
   {
     ProfScope ps(b, "moe_count");
-    hipLaunchKernelGGL(k_moe_count, dim3(nblk), dim3(256), 0, b->stream, idx, m.counts, T, K, E);
+    hipLaunchKernelGGL(k_moe_count, dim3(nblk), dim3(RBLK), 0, b->stream, idx, m.counts, T, K, E);
     PF_HIP(hipGetLastError());
   }
   {
@@ -1049,7 +1068,7 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
   }
   {
     ProfScope ps(b, "moe_scatter");
-    hipLaunchKernelGGL(k_moe_scatter, dim3(nblk), dim3(256), 0, b->stream, idx, m.blk_off, m.slot_token, m.slot_of,
+    hipLaunchKernelGGL(k_moe_scatter, dim3(nblk), dim3(RBLK), 0, b->stream, idx, m.blk_off, m.slot_token, m.slot_of,
                        T, K, E);
     PF_HIP(hipGetLastError());
   }
