@@ -411,17 +411,46 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       auto at = [&](int c) -> float {
         return *reinterpret_cast<const float*>(rb + (((c >> 2) ^ (row & SO::SWM)) << 4) + (c & 3) * 4);
       };
-      float V[4];
-      int I[4];
-      topk_insertion<4>([&](int c) { return at(SEG * part + c); }, SEG, V, I);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) I[k] += SEG * part;
       bool nan = false;
 #pragma unroll
       for (int u = 0; u < SEG / 4; ++u) {
         const f4_t q = *reinterpret_cast<const f4_t*>(rb + ((((SEG / 4) * part + u) ^ (row & SO::SWM)) << 4));
         nan = nan | (q[0] != q[0]) | (q[1] != q[1]) | (q[2] != q[2]) | (q[3] != q[3]);
       }
+      float V[4];
+      int I[4];
+      if constexpr (SEG == 8) {
+        // short segments: branch-free selection on (value, index) keys;
+        // a row with a NaN takes the sequential path below
+        uint64_t ka[4], kb[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          ka[c] = topk_key(at(SEG * part + c), SEG * part + c);
+          kb[c] = topk_key(at(SEG * part + 4 + c), SEG * part + 4 + c);
+        }
+        topk_sort4(ka);
+        topk_sort4(kb);
+        topk_merge4(ka, kb);
+#pragma unroll
+        for (int sft = 1; sft < TPR; sft <<= 1) {
+          nan = nan | (__shfl_xor((int)nan, sft, 64) != 0);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = __shfl_xor((uint32_t)ka[k], sft, 64);
+            const uint32_t hi = __shfl_xor((uint32_t)(ka[k] >> 32), sft, 64);
+            kb[k] = ((uint64_t)hi << 32) | lo;
+          }
+          topk_merge4(ka, kb);  // keys are distinct: both threads of a pair get the same list
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          I[k] = topk_key_index(ka[k]);
+          V[k] = at(I[k]);
+        }
+      } else {
+      topk_insertion<4>([&](int c) { return at(SEG * part + c); }, SEG, V, I);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) I[k] += SEG * part;
 #pragma unroll
       for (int sft = 1; sft < TPR; sft <<= 1) {
         nan = nan | (__shfl_xor((int)nan, sft, 64) != 0);
@@ -471,6 +500,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
           V[k] = RV[k];
           I[k] = RI[k];
         }
+      }
       }
       if (part == 0 && row < rows) {
         if (nan) topk_insertion<4>(at, 128, V, I);

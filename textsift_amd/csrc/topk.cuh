@@ -34,6 +34,44 @@ __device__ void topk_insertion(Row x, int E, float* V, int* I) {
   }
 }
 
+// Branch-free form for short segments: a logit and its index as one 64-bit
+// key, larger = earlier in the insertion order (value descending, then
+// index ascending; -0 and +0 compare equal there, so -0 is keyed as +0).
+// Keys of distinct indices are distinct. Only for rows without NaNs.
+__device__ __forceinline__ uint64_t topk_key(float v, int idx) {
+  const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0
+  const uint32_t o = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);  // order-preserving
+  return ((uint64_t)o << 32) | (uint32_t)(0xFFFF - idx);
+}
+__device__ __forceinline__ int topk_key_index(uint64_t k) { return 0xFFFF - (int)(uint32_t)(k & 0xFFFFu); }
+
+// compare-exchange: a keeps the larger key
+__device__ __forceinline__ void topk_ce(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+// four keys sorted descending
+__device__ __forceinline__ void topk_sort4(uint64_t* k) {
+  topk_ce(k[0], k[1]);
+  topk_ce(k[2], k[3]);
+  topk_ce(k[0], k[2]);
+  topk_ce(k[1], k[3]);
+  topk_ce(k[1], k[2]);
+}
+
+// the 4 largest of two descending lists of 4 (into a), descending: the
+// pairwise maxima of a and reversed b form a bitonic sequence holding them
+__device__ __forceinline__ void topk_merge4(uint64_t* a, const uint64_t* b) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = a[i] > b[3 - i] ? a[i] : b[3 - i];
+  topk_ce(a[0], a[2]);
+  topk_ce(a[1], a[3]);
+  topk_ce(a[0], a[1]);
+  topk_ce(a[2], a[3]);
+}
+
 // Routing weights of the K selected logits V (sorted as above): softmax
 // with libm exp, times wscale; written with the expert ids to idx / w.
 template <int K>
