@@ -89,7 +89,14 @@ __global__ __launch_bounds__(256) void k_gemm_int4(GemmArgs p) {
   const int l16 = lane & 15, lg = lane >> 4;
 
   const int n_tiles = (p.N + BN - 1) / BN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  // grouped: the XCD remap over the workgroups that have tiles (the grid
+  // covers the largest possible tile list)
+  int active = (int)gridDim.x;
+  if constexpr (GROUPED) {
+    active = min(active, *p.num_tiles * n_tiles);
+    if ((int)blockIdx.x >= active) return;
+  }
+  const int bid = xcd_remap(blockIdx.x, active);
   const int nt = bid % n_tiles;
   const int tt = bid / n_tiles;
   int expert = 0, row0, rows;

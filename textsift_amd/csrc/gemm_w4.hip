@@ -134,7 +134,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   const int l16 = lane & 15, lg = lane >> 4;
 
   const int n_tiles = (p.N + BN - 1) / BN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  // Grouped: the grid covers the largest possible tile list; only the first
+  // num_tiles x n_tiles workgroups have work. Those are spread round-robin
+  // over the XCDs by the hardware, and the XCD remap is taken over them alone
+  // (over the whole grid it would put all the work on the first XCDs).
+  int active = (int)gridDim.x;
+  if constexpr (GROUPED) {
+    active = min(active, *p.num_tiles * n_tiles);
+    if ((int)blockIdx.x >= active) return;
+  }
+  const int bid = xcd_remap(blockIdx.x, active);
   const int nt = bid % n_tiles;
   const int tt = bid / n_tiles;
   int expert = 0, row0, rows;
