@@ -320,6 +320,26 @@ __device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx
   __syncthreads();
 }
 
+// The grouped-GEMM tile list (expert, row0, rows), written by all threads of
+// the workgroup: tile ti belongs to the last expert whose first tile (tile0,
+// an exclusive prefix over experts) is <= ti. row0 = expert row offsets
+// (exclusive prefix), grand = total rows. (One thread per expert would write
+// a hot expert's hundreds of tiles alone.)
+__device__ __forceinline__ void moe_write_tiles(const int32_t* tile0, const int32_t* row0, int grand, int E,
+                                                int ntiles, int tile_t, int32_t* __restrict__ tiles) {
+  for (int ti = threadIdx.x; ti < ntiles; ti += blockDim.x) {
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tile0[mid] <= ti) lo = mid;
+      else hi = mid - 1;
+    }
+    const int total = (lo + 1 < E ? row0[lo + 1] : grand) - row0[lo];
+    const int r = (ti - tile0[lo]) * tile_t;
+    reinterpret_cast<int4*>(tiles)[ti] = int4{lo, row0[lo] + r, min(tile_t, total - r), 0};
+  }
+}
+
 // counts[blk][e] = tokens of block blk routed to expert e.
 __global__ __launch_bounds__(RBLK) void k_moe_count(const int32_t* __restrict__ idx, int32_t* __restrict__ counts,
                                                     int T, int K, int E) {
@@ -347,7 +367,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __rest
                                                            int32_t* __restrict__ num_tiles, int nblk, int E, int E2,
                                                            int tile_t) {
   __shared__ int32_t part[SCAN_THREADS];  // [j][e] partial sums, then exclusive prefixes over j
-  __shared__ int32_t tot[257], ntl[256];
+  __shared__ int32_t tot[257], ntl[257];
   if (threadIdx.x < 256) {
     tot[threadIdx.x] = 0;
     ntl[threadIdx.x] = 0;
@@ -423,11 +443,13 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __rest
     }
     if (l == 63) {
       tot[256] = ce;  // grand total
+      ntl[256] = ne;
       expert_off[E] = ce;
       *num_tiles = ne;
     }
   }
   __syncthreads();
+  moe_write_tiles(ntl, tot, tot[256], E, ntl[256], tile_t, tiles);
   if (e < E) {
     const int base = tot[e];
     if (j == 0) expert_off[e] = base;
@@ -454,13 +476,6 @@ __global__ __launch_bounds__(SCAN_THREADS) void k_moe_scan(const int32_t* __rest
     for (; b < b1; ++b) {
       blk_off[(size_t)b * E + e] = run;
       run += counts[(size_t)b * E + e];
-    }
-    if (j == 0) {
-      const int total = (e + 1 < E ? tot[e + 1] : tot[256]) - base;
-      int tix = ntl[e];
-      for (int r = 0; r < total; r += tile_t, ++tix) {
-        reinterpret_cast<int4*>(tiles)[tix] = int4{e, base + r, min(tile_t, total - r), 0};
-      }
     }
   }
 }
@@ -506,7 +521,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
                                                           int32_t* __restrict__ num_tiles, int T, int K, int E,
                                                           int tile_t) {
   __shared__ uint32_t bits[256 * BWS];
-  __shared__ int32_t off[256], wsum[2][RBLK / 64];
+  __shared__ int32_t off[256], toff[256], wsum[2][RBLK / 64];
   moe_block_bitmap(idx, bits, 0, T, K, E);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // rows c and tiles n of expert e = tid; inclusive scans within the wave
@@ -539,18 +554,17 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
     nt += wsum[1][w];
   }
   const int base = cb + ci - c;  // exclusive prefix of rows
-  int tix = nbase + ni - n;      // exclusive prefix of tiles
   if (tid < E) {
     off[tid] = base;
+    toff[tid] = nbase + ni - n;  // exclusive prefix of tiles
     expert_off[tid] = base;
-    for (int r = 0; r < c; r += tile_t, ++tix)
-      reinterpret_cast<int4*>(tiles)[tix] = int4{tid, base + r, min(tile_t, c - r), 0};
   }
   if (tid == 0) {
     expert_off[E] = ct;
     *num_tiles = nt;
   }
   __syncthreads();
+  moe_write_tiles(toff, off, ct, E, nt, tile_t, tiles);
   if (tid >= T) return;
   const int wl = tid >> 5;
   const uint32_t below = (1u << (tid & 31)) - 1u;
