@@ -320,6 +320,23 @@ __device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx
   __syncthreads();
 }
 
+// pre[e][w] = tokens of the block routed to e among words 0 .. w-1 of the
+// bitmap (so a token's rank is pre[e][w] plus a popcount within its word)
+__device__ __forceinline__ void moe_word_prefix(const uint32_t* bits, uint16_t* pre, int E) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    uint32_t w[RBLK / 32];
+#pragma unroll
+    for (int u = 0; u < RBLK / 32; ++u) w[u] = bits[e * BWS + u];
+    int run = 0;
+#pragma unroll
+    for (int u = 0; u < RBLK / 32; ++u) {
+      pre[e * BWS + u] = (uint16_t)run;
+      run += __popc(w[u]);
+    }
+  }
+  __syncthreads();
+}
+
 // The grouped-GEMM tile list (expert, row0, rows), written by all threads of
 // the workgroup: tile ti belongs to the last expert whose first tile (tile0,
 // an exclusive prefix over experts) is <= ti. row0 = expert row offsets
@@ -492,6 +509,8 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
   const int t0 = blk * RBLK;
   const int nt = min(RBLK, T - t0);
   moe_block_bitmap(idx, bits, t0, nt, K, E);
+  __shared__ uint16_t pre[256 * BWS];
+  moe_word_prefix(bits, pre, E);
   const int tl = threadIdx.x;
   if (tl >= nt) return;
   const int wl = tl >> 5;
@@ -500,9 +519,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_scatter(const int32_t* __restrict_
     const size_t i = (size_t)(t0 + tl) * K + k;
     const int e = idx[i];
     if ((unsigned)e >= (unsigned)E) continue;
-    const uint32_t* be = bits + e * BWS;
-    int rank = __popc(be[wl] & below);
-    for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
+    const int rank = pre[e * BWS + wl] + __popc(bits[e * BWS + wl] & below);
     const int pos = blk_off[(size_t)blk * E + e] + rank;
     slot_token[pos] = t0 + tl;
     slot_of[i] = pos;
@@ -565,6 +582,8 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
   }
   __syncthreads();
   moe_write_tiles(toff, off, ct, E, nt, tile_t, tiles);
+  __shared__ uint16_t pre[256 * BWS];
+  moe_word_prefix(bits, pre, E);
   if (tid >= T) return;
   const int wl = tid >> 5;
   const uint32_t below = (1u << (tid & 31)) - 1u;
@@ -572,9 +591,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
     const size_t i = (size_t)tid * K + k;
     const int e = idx[i];
     if ((unsigned)e >= (unsigned)E) continue;
-    const uint32_t* be = bits + e * BWS;
-    int rank = __popc(be[wl] & below);
-    for (int w = 0; w < wl; ++w) rank += __popc(be[w]);
+    const int rank = pre[e * BWS + wl] + __popc(bits[e * BWS + wl] & below);
     const int pos = off[e] + rank;
     slot_token[pos] = tid;
     slot_of[i] = pos;
