@@ -305,11 +305,12 @@ def test_fused_router_topk_bit_exact(kind):
     assert np.allclose(rw, w_ref, rtol=0.0, atol=2e-7, equal_nan=True)
 
 
-@pytest.mark.parametrize("B,T", [(1, 300), (8, 2048)], ids=["two-kernels", "fused"])
+@pytest.mark.parametrize("B,T", [(1, 300), (8, 2048)], ids=["norm-in-router", "fused"])
 def test_o_residual_norm_vs_oracle(small, B, T):
-    """The O projection, residual add and RMSNorm (fp16 numerics): as the O
-    GEMM and add_rmsnorm kernels for small batches, as one kernel with the
-    add and the norm in its epilogue from 16384 rows on. The new residual h2
+    """The O projection, residual add and RMSNorm (fp16 numerics): below
+    16384 rows the O GEMM, with the add and the norm done by the router
+    GEMM on its way in (its 16-token tile holds whole rows); from 16384 rows
+    on one kernel with the add and the norm in its epilogue. The new residual h2
     and the normalised xn against the oracle's MatMulNBits (fp16 out,
     zig/wasm_exports.zig:560-707) and add_rmsnorm (:288-350) on the same
     inputs (the GPU's attention output and the block's input, the embedding)."""

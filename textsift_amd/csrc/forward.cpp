@@ -333,6 +333,11 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   // dense GEMMs of at most SMALL_M rows (O and the classifier 2x, the
   // router 8x: measured crossovers) take the all-K 16-token tile
   auto small_dense = [&](int k, int limit = SMALL_M) { return M <= limit && small_k((size_t)k); };
+  // O projection: one kernel with the add + norm from 16384 rows; below, the
+  // O GEMM, and the add + norm either in the router GEMM (its 16-token tile
+  // holds whole 640-wide rows) or as its own kernel
+  const bool fused_o = f16 && D == 640 && (Hq * hd == 640 || Hq * hd == 896) && M >= 16384;
+  const bool norm_in_router = f16 && !fused_o && D == 640 && small_dense(D, 8 * SMALL_M);
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
@@ -382,23 +387,25 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         // per CU and latency-bound, so it pays only once there are enough
         // rows to fill the chip (measured: 87 vs 97 us at 32768 rows; 44 vs
         // 40 us at 8192 and 40 vs 31 us at 64 for the two-kernel form)
-        if (D == 640 && (Hq * hd == 640 || Hq * hd == 896) && M >= 16384) {
+        if (fused_o) {
           gemm_w4_add_rmsnorm(b, a, h, L.ln_post, s.h2, s.xn_hi, c.eps);
         } else {
           const bool sm = small_dense(Hq * hd, 2 * SMALL_M);
           gemm_w4(b, a, XKind::F16, Epi::F16, false, sm ? 16 : 128, sm ? 1 : 4, "gemm_o");
-          add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
+          if (!norm_in_router) add_rms_norm_f16(b, h, s.o, L.ln_post, s.h2, s.xn_hi, M, D, c.eps);
         }
       } else {
         gemm_int4(b, a, XKind::F16, Epi::F16, false, 128, "gemm_o");
         add_rms_norm_split(b, h, s.o, L.ln_post, s.h2, s.xn_hi, s.xn_lo, M, D, c.eps);
       }
     }
-    record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
-    record_tap(m, "xn2." + tag, s.xn_hi, (size_t)M * D * 2);
     {
       GemmArgs a;
       a.x = s.xn_hi; a.x_lo = s.xn_lo; a.ldx = D;
+      if (norm_in_router) {  // the post-attention add + norm on the router's way in
+        a.x = s.o;
+        a.nrm_res = h; a.nrm_gamma = L.ln_post; a.nrm_h = s.h2; a.nrm_xn = s.xn_hi; a.nrm_eps = c.eps;
+      }
       a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
       a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
       // fp16 numerics with the model's 128 experts and top-4: the router
@@ -416,6 +423,8 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       }
       if (!fused_topk) router_topk(b, s.rlogits, s.ridx, s.rw, M, E, K, 1.0f);
     }
+    record_tap(m, "h2." + tag, s.h2, (size_t)M * D * 2);
+    record_tap(m, "xn2." + tag, s.xn_hi, (size_t)M * D * 2);
     record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
     record_tap(m, "ridx." + tag, s.ridx, (size_t)M * K * 4);
     record_tap(m, "rw." + tag, s.rw, (size_t)M * K * 4);

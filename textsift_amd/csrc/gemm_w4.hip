@@ -118,7 +118,7 @@ struct StagedOut {
 // and weights are loaded at once, so a workgroup waits for memory once
 // instead of once per chunk (the latency that dominates when a GEMM is a few
 // workgroups).
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0>
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
@@ -287,8 +287,63 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       load_x(c, c);
       load_w(c, wall[c], szall[c]);
     }
+    if constexpr (NORM) {
+      // the residual rows into buffers CT .. 2 CT - 1, in the same layout
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int m = 0; m < XI; ++m)
+          copy16_to_lds(p.nrm_res + xoff[m] + c * KC, (lds_ptr_t)(xs_lds + (CT + c) * PLANE + (m * NW + wave) * 512));
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if constexpr (NORM) {
+      // 16 threads per row, each one 8-value unit of every chunk: h2 =
+      // fp16(o + res), the row's sum of squares of the f32 sums, xn =
+      // fp16(h2 inv_rms gamma) stored to memory and over o for the MFMAs
+      static_assert(BT * 16 == 64 * NW && XS == 1, "row normalisation: 16 threads per row, one plane");
+      const int r = tid >> 4, q = tid & 15;
+      const int slot = (q ^ (r & 15)) << 3;
+      u4_t hs[CT];
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const h8_t o8 = *reinterpret_cast<const h8_t*>(xs_lds + c * PLANE + r * KC + slot);
+        const h8_t r8 = *reinterpret_cast<const h8_t*>(xs_lds + (CT + c) * PLANE + r * KC + slot);
+        float sv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          sv[i] = (float)o8[i] + (float)r8[i];
+          ss += sv[i] * sv[i];
+        }
+        const u2_t lo = to_f16x4(sv), hi = to_f16x4(sv + 4);
+        hs[c] = u4_t{lo.x, lo.y, hi.x, hi.y};
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+      const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)(CT * KC)) + p.nrm_eps);
+      const bool store = r < rows;
+      const size_t orow = (size_t)(row0 + r) * (CT * KC);
+      __syncthreads();  // every thread has read its o and residual units
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        const int col = c * KC + q * 8;
+        const u4_t gw = *reinterpret_cast<const u4_t*>(p.nrm_gamma + col);
+        const h8_t h8 = __builtin_bit_cast(h8_t, hs[c]);
+        const h8_t g8 = __builtin_bit_cast(h8_t, gw);
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = (float)h8[i] * inv_rms * (float)g8[i];
+        const u2_t lo = to_f16x4(y), hi = to_f16x4(y + 4);
+        const u4_t xv = u4_t{lo.x, lo.y, hi.x, hi.y};
+        *reinterpret_cast<u4_t*>(xs_lds + c * PLANE + r * KC + slot) = xv;
+        if (store) {
+          *reinterpret_cast<u4_t*>(p.nrm_h + orow + col) = hs[c];
+          *reinterpret_cast<u4_t*>(p.nrm_xn + orow + col) = xv;
+        }
+      }
+      __syncthreads();
+    }
   } else {
     load_x(0, 0);
     load_w(0, wraw, sz);
@@ -555,7 +610,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 }
 
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0>
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false>
 void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   constexpr int BN = NW * WF * 16;
   const int n_tiles = (a.N + BN - 1) / BN;
@@ -566,17 +621,17 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   PF_CHECK(CT == 0 || a.K == CT * KC, "gemm_w4: K does not match the tile's compile-time chunk count");
   // activation buffers: two (double buffering) or all CT chunks, plus the
   // RoPE table's plane when every chunk buffer is taken
-  constexpr int NBUF = CT > 0 ? CT + (EPI == Epi::ROPE_F16 ? 1 : 0) : 2;
+  constexpr int NBUF = CT > 0 ? (NORM ? 2 * CT : CT) + (EPI == Epi::ROPE_F16 ? 1 : 0) : 2;
   const size_t lds = std::max((size_t)NBUF * XS * BT * KC * sizeof(uint16_t),
                               StagedOut<WF, BT, EPI, NW>::OK ? StagedOut<WF, BT, EPI, NW>::LDS : (size_t)0);
   static bool attr_set = false;  // per template instance
   if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT>),
+    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
   ProfScope ps(b, name);
-  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT>), dim3((unsigned)grid), dim3(64 * NW), lds,
+  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>), dim3((unsigned)grid), dim3(64 * NW), lds,
                      b->stream, a);
   PF_HIP(hipGetLastError());
 }
@@ -615,6 +670,14 @@ void dispatch_grouped(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped
 // 16-token tile with all of K loaded at once: K = 640 or 896 (5 or 7 chunks)
 template <int WF>
 void dispatch_small(pfhip_backend* b, const GemmArgs& a, Epi epi, bool grouped, const char* name) {
+  if (a.nrm_res) {  // the router's residual add + norm on the way in
+    if constexpr (WF == 2) {
+      if (!grouped && a.K == 5 * KC && epi == Epi::F32_TOPK)
+        return launch<2, 16, 1, Epi::F32_TOPK, false, 4, 5, true>(b, a, name);
+      if (!grouped && a.K == 5 * KC && epi == Epi::F32) return launch<2, 16, 1, Epi::F32, false, 4, 5, true>(b, a, name);
+    }
+    throw Error("gemm_w4: the input norm is built for the 16-token router tile, K = 640");
+  }
   switch (a.K / KC) {
     case 5: return dispatch_grouped<WF, 16, 4, 5>(b, a, epi, grouped, name);
     case 7: return dispatch_grouped<WF, 16, 4, 7>(b, a, epi, grouped, name);
@@ -700,6 +763,11 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, g, epi, grouped, prof_name);
+  if (a.nrm_res)
+    PF_CHECK(a.nrm_gamma && a.nrm_h && a.nrm_xn && a.ldx == a.K && tile_t == 16 &&
+                 ((reinterpret_cast<uintptr_t>(a.nrm_res) | reinterpret_cast<uintptr_t>(a.nrm_gamma) |
+                   reinterpret_cast<uintptr_t>(a.nrm_h) | reinterpret_cast<uintptr_t>(a.nrm_xn)) & 15) == 0,
+             "gemm_w4: input norm needs residual, gamma and outputs (16-byte aligned, rows of K) on the 16-token tile");
   if (tile_t == 16 && wf == 1) return dispatch_small<1>(b, g, epi, grouped, prof_name);
   if (tile_t == 16 && wf == 2) return dispatch_small<2>(b, g, epi, grouped, prof_name);
   throw Error("gemm_w4: unsupported (tile_t, wf) = (" + std::to_string(tile_t) + ", " + std::to_string(wf) + ")");

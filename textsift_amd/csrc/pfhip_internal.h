@@ -123,6 +123,14 @@ struct GemmArgs {
   float* topk_w = nullptr;
   int topk_k = 0;
   float topk_wscale = 1.0f;
+  // Residual add + RMSNorm on the way in (gemm_w4, 16-token tile, K == 640):
+  // x is the fp16 O projection output o; the kernel forms h2 = fp16(o + res)
+  // and xn = fp16(h2 * inv_rms(o + res) * gamma), writes both, and multiplies xn.
+  const uint16_t* nrm_res = nullptr;
+  const uint16_t* nrm_gamma = nullptr;
+  uint16_t* nrm_h = nullptr;
+  uint16_t* nrm_xn = nullptr;
+  float nrm_eps = 0.0f;
   // gemm_w4: stage the output tile through LDS and store whole 16-byte units
   // (set by gemm_w4 itself when the output layout allows it)
   int out_staged = 0;
