@@ -84,7 +84,7 @@ def test_exp_approx_fast_exhaustive(be):
 # ---------------------------------------------------------------- MFMA operand layout
 
 def test_mfma_16x16x32_f16_layout(be):
-    """Checks the lane layout assumed by every MFMA kernel (common.cuh) with
+    """Checks the lane layout assumed by every MFMA kernel (common.h) with
     small integers, for which the product is exact."""
     rng = np.random.default_rng(0)
     A = rng.integers(-8, 8, (16, 32)).astype(np.float16)

@@ -23,8 +23,8 @@
 //    reference's values, not just its mathematics.
 //  * p is normalised before P.V (as the reference does) and enters the
 //    MFMA as an fp16 hi + lo pair, so P.V carries ~22 significant bits.
-#include "common.cuh"
-#include "epilogue.cuh"
+#include "common.h"
+#include "epilogue.h"
 #include "pfhip_internal.h"
 
 namespace pf {

@@ -1,4 +1,4 @@
-// common.cuh — device helpers shared by the gfx950 kernels.
+// common.h — device helpers shared by the gfx950 kernels.
 //
 // Numerics follow the reference's WASM path
 // (packages/textsift/src/zig/math.zig, zig/wasm_exports.zig): every kernel

@@ -1,4 +1,4 @@
-// epilogue.cuh — output stage shared by the int4 GEMM kernels.
+// epilogue.h — output stage shared by the int4 GEMM kernels.
 //
 // A lane holds 4 consecutive output columns n..n+3 of one output row (the
 // GEMMs are computed transposed). The split numerics' conversions to fp16
@@ -8,7 +8,7 @@
 // `_native` forms: the hardware conversions and fp16 arithmetic the
 // reference's GPU shaders perform.
 #pragma once
-#include "common.cuh"
+#include "common.h"
 #include "pfhip_internal.h"
 
 namespace pf {

@@ -27,8 +27,8 @@
 //  * Grouped mode: tiles come from a device list of (expert, row0, rows)
 //    built by the MoE routing kernels; weights are offset per expert and
 //    activation rows may be gathered through row_map.
-#include "common.cuh"
-#include "epilogue.cuh"
+#include "common.h"
+#include "epilogue.h"
 #include "pfhip_internal.h"
 
 namespace pf {

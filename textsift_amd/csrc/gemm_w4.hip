@@ -33,10 +33,10 @@
 //  * The GEMM is computed transposed (D = W . X^T) as in gemm_int4.hip, so
 //    each lane ends with 4 consecutive output columns of one token and the
 //    RoPE / SwiGLU epilogues are lane-local.
-#include "common.cuh"
-#include "epilogue.cuh"
+#include "common.h"
+#include "epilogue.h"
 #include "pfhip_internal.h"
-#include "topk.cuh"
+#include "topk.h"
 
 namespace pf {
 

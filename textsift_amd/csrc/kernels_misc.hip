@@ -3,10 +3,10 @@
 // router top-k, the MoE routing plan (a deterministic counting sort) and the
 // MoE combine. Reference semantics: packages/textsift/src/zig/wasm_exports.zig
 // (line ranges cited per kernel).
-#include "common.cuh"
-#include "epilogue.cuh"
+#include "common.h"
+#include "epilogue.h"
 #include "pfhip_internal.h"
-#include "topk.cuh"
+#include "topk.h"
 
 namespace pf {
 
@@ -231,7 +231,7 @@ __global__ void k_rope(uint16_t* qk, const uint16_t* cs, const uint16_t* sn, int
 
 // ----------------------------------------------------------------------------
 // Router top-k + softmax (topk_partial_f32 :367-426, softmax_f32 :919-958;
-// the insertion order and the weights are in topk.cuh): output sorted by
+// the insertion order and the weights are in topk.h): output sorted by
 // logit descending, ties keep the lower expert id first.
 constexpr int MAXK = 8;
 // One wave per token; lane l holds logits l, l+64, l+128, l+192. Without

@@ -1,9 +1,9 @@
-// topk.cuh — the reference's router top-k (topk_partial_f32,
+// topk.h — the reference's router top-k (topk_partial_f32,
 // packages/textsift/src/zig/wasm_exports.zig:367-426) and the softmax over
 // the K selected logits (softmax_f32 :919-958), shared by the stand-alone
 // top-k kernel and the router GEMM's fused epilogue.
 #pragma once
-#include "common.cuh"
+#include "common.h"
 
 namespace pf {
 
