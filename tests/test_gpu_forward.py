@@ -166,6 +166,47 @@ def test_full_model_forward_vs_oracle(full_ref, precision):
         be.dispose()
 
 
+@pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
+def test_full_batch_16x2048(full_ref, precision):
+    """The benchmarked launch set (BASELINE config 5 at its stated batch):
+    16 sequences x 2048 tokens in one forward, i.e. 32768 rows, where the
+    forward takes the fused O + residual + RMSNorm kernel, the router GEMM's
+    128-row top-4 tile and 128-row expert tiles. Sequence 0 carries full_ref's
+    ids and sequence 15 is checked against its own oracle forward: rel-err
+    < 2e-3, argmax agreement >= 99.9 %, identical spans. Every sequence's
+    logits also equal those of its own single-sequence forward (2048 rows:
+    the O GEMM with the norm in the router's 16-row tile, 64-row expert
+    tiles) bit for bit, so no result depends on the batch it was run in."""
+    w, ids0, ref0 = full_ref
+    T = ids0.size
+    B = 16
+    ids = synth.token_ids(1016, B * T).reshape(B, T)
+    ids[0] = ids0
+    be = HipBackend(w, precision=precision)
+    be.warmup()
+    try:
+        got = be.forward_batch(ids)
+        differ = []
+        for b in range(B):
+            one = be.forward(ids[b], np.ones(T, np.uint8)).as_matrix()
+            if not np.array_equal(got[b].view(np.uint32), one.view(np.uint32)):
+                differ.append((b, float(np.mean(got[b] != one))))
+        print(f"16x2048 precision={precision}: sequences differing from their single forward: {differ}")
+        assert not differ
+    finally:
+        be.dispose()
+    ref15 = f16(oracle.model_forward(PF_CONFIG, w, ids[15], n_threads=8)).astype(np.float32)
+    for b, ref in ((0, ref0), (15, ref15)):
+        err = rel_err_norm(got[b], ref)
+        agree = np.mean(np.argmax(got[b], 1) == np.argmax(ref, 1))
+        same, rep = span_parity(got[b], ref, _synthetic_chunk(T))
+        print(f"16x2048 precision={precision} sequence {b}: rel-err {err:.3e}, argmax agreement {agree:.5f}, "
+              f"spans identical {same} {rep}")
+        assert err < 2e-3
+        assert agree >= 0.999
+        assert same or near_tie_only(rep, T)
+
+
 def test_detect_spans_vs_oracle(small):
     """detect() through the HIP backend (full-length chunks in one batched
     forward) gives the spans of the oracle's logits pushed through the same

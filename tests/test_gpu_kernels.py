@@ -459,9 +459,7 @@ def test_moe_route_permutation_bit_exact(be, T, E, tile):
 def zipf_router(T, D, E, seed):
     """fp16 router W [D][E] ~ N(0, 0.02) and a bias that skews the realised
     load towards Zipf(1.1)."""
-    w = synth.to_fp16_bits(synth.normal(seed, D * E, 0, 0.02)).reshape(D, E)
-    bias = synth.to_fp16_bits(1.1 * -np.log(np.arange(1, E + 1)) * 0.35)
-    return w, bias
+    return synth.zipf_router(seed, D, E)
 
 
 @pytest.mark.parametrize("T,E", [(2048, 128), (37, 16)])

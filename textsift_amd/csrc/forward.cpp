@@ -24,12 +24,26 @@
 // positions restart per sequence. Weights stay in the ONNX byte layouts;
 // finalize() concatenates q/k/v into one [1152][K] weight so the three
 // projections are one GEMM.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
 #include "pfhip_internal.h"
 
 using namespace pf;
+
+namespace pf {
+// Expert tile rows for the grouped GEMMs, from the mean rows per expert:
+// 128 from 256 on, 64 below, 16 (the all-K tile, fp16 numerics, K = 640 or
+// 896) below 32; fragments per wave 4, 5 and 1 respectively.
+ExpertTile expert_tile(int M, int topk, int experts, bool fp16, int D, int F) {
+  const int per_expert = (int)((long)M * topk / experts);
+  if (per_expert >= 256) return {128, 4};
+  const auto small_k = [](int k) { return k == 640 || k == 896; };
+  if (fp16 && small_k(D) && small_k(F) && per_expert < 32) return {16, 1};
+  return {64, 5};
+}
+}  // namespace pf
 
 namespace {
 
@@ -200,6 +214,20 @@ void build_rope_tables(const pfhip_model_config& c, int T, std::vector<uint16_t>
     }
 }
 
+// The kernels address activation rows with 32-bit element offsets: every
+// [rows][width] array of the forward must hold fewer than 2^31 elements
+// (the widest are the routed [M * topk][max(hidden, dff)] expert planes).
+// Checked before any scratch is allocated or kernel launched.
+void check_row_limits(const pfhip_model_config& c, size_t M) {
+  const size_t S = M * c.topk;
+  const size_t NQKV = (size_t)(c.heads + 2 * c.kv_heads) * c.head_dim;
+  const size_t widest = std::max({M * NQKV, M * c.heads * c.head_dim, M * c.experts, S * c.hidden, S * c.dff,
+                                  M * c.classes});
+  PF_CHECK(widest < ((size_t)1 << 31),
+           "batch * seq_len too large for this model: a [rows][width] activation array of " +
+               std::to_string(widest) + " elements exceeds the kernels' 32-bit offsets");
+}
+
 struct Scr {
   uint16_t *h0, *h1, *h2, *qkv, *att, *o, *logits16;
   uint16_t *xn_hi, *xn_lo, *glu_hi, *glu_lo;
@@ -212,16 +240,12 @@ struct Scr {
 // waits on memory once instead of once per 128-wide K chunk, which is what
 // a GEMM of a few workgroups costs. fp16 numerics only.
 constexpr int SMALL_M = 2048;           // dense GEMMs: rows up to this
-constexpr int SMALL_PER_EXPERT = 32;    // expert GEMMs: mean rows per expert below this
 bool small_k(size_t K) { return K == 640 || K == 896; }
 
-// Expert tile rows for the grouped GEMMs, from the mean rows per expert:
-// 128 from 256 on, 64 below, 16 (the all-K tile) below SMALL_PER_EXPERT.
 int tile_for(const pfhip_model_config& c, int M) {
-  const int per_expert = M * (int)c.topk / (int)c.experts;
-  if (per_expert >= 256) return 128;
-  const bool small = c.precision == PFHIP_PRECISION_FP16 && small_k(c.hidden) && small_k(c.dff);
-  return small && per_expert < SMALL_PER_EXPERT ? 16 : 64;
+  return expert_tile(M, (int)c.topk, (int)c.experts, c.precision == PFHIP_PRECISION_FP16, (int)c.hidden,
+                     (int)c.dff)
+      .t;
 }
 
 size_t scratch_layout(const pfhip_model_config& c, int M, Scr* s, void* base) {
@@ -329,7 +353,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
 
   const bool f16 = c.precision == PFHIP_PRECISION_FP16;
   // GEMM tiles of the fp16 path: (tokens, 16-row fragments per wave)
-  const int gw_t = tt, gw_f = tt == 128 ? 4 : (tt == 64 ? 5 : 1);
+  const int gw_t = tt, gw_f = expert_tile(M, K, E, f16, D, F).wf;
   // dense GEMMs of at most SMALL_M rows (O and the classifier 2x, the
   // router 8x: measured crossovers) take the all-K 16-token tile
   auto small_dense = [&](int k, int limit = SMALL_M) { return M <= limit && small_k((size_t)k); };
@@ -646,10 +670,11 @@ int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* 
                                uint32_t seq_len, pfhip_buffer* logits, char* err, size_t cap) {
   try {
     PF_CHECK(m && ids && logits, "null argument");
-    PF_CHECK(m->finalized, "call pfhip_model_finalize() first");
     PF_CHECK(batch >= 1 && seq_len >= 1, "batch and seq_len must be positive");
     const size_t M = (size_t)batch * seq_len;
     PF_CHECK(M <= (1u << 22), "batch * seq_len too large");
+    check_row_limits(m->cfg, M);
+    PF_CHECK(m->finalized, "call pfhip_model_finalize() first");
     PF_CHECK(ids->size >= M * 4, "ids buffer too small");
     PF_CHECK(!mask || mask->size >= M, "mask buffer too small");
     PF_CHECK(logits->size >= M * m->cfg.classes * 4, "logits buffer too small");

@@ -311,6 +311,9 @@ void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grou
   if (epi == Epi::ROPE_F16) PF_CHECK(!grouped && (long)a.M < (1L << 31), "RoPE epilogue: dense rows below 2^31");
   if (grouped) PF_CHECK(a.tiles && a.num_tiles && a.max_tiles > 0, "gemm_int4: grouped mode needs a tile list");
   else PF_CHECK(a.M >= 0, "gemm_int4: M must be non-negative");
+  // activation rows are addressed with 32-bit element offsets (grouped: a.M
+  // slots bound every row the tile list or the row map can name)
+  PF_CHECK((long)a.M * a.ldx < (1L << 31), "gemm_int4: activation offsets exceed 32 bits");
   const bool split = xk == XKind::SPLIT;
   if (tile_t == 64) {
     if (split) {

@@ -298,48 +298,62 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (NORM) {
-      // 16 threads per row, each one 8-value unit of every chunk: h2 =
-      // fp16(o + res), the row's sum of squares of the f32 sums, xn =
-      // fp16(h2 inv_rms gamma) stored to memory and over o for the MFMAs
-      static_assert(BT * 16 == 64 * NW && XS == 1, "row normalisation: 16 threads per row, one plane");
+      // 16 threads per row: h2 = fp16(o + res), the row's sum of squares of
+      // the f32 sums, xn = fp16(h2 inv_rms gamma) stored to memory and over o
+      // for the MFMAs. The sum of squares is taken in exactly the order of
+      // the fused O kernel's epilogue (k_gemm_w4_rownorm below), so both
+      // forms give bit-identical h2 and xn and a sequence's result does not
+      // depend on the batch size that selects the form: there, lane group lg
+      // of wave w sums fma(s, s, .) over columns (5 w + f) 16 + 4 lg + 0..3
+      // for f = 0..4 in that order, lane groups combine as (P0 + P1) +
+      // (P2 + P3) and the 8 wave sums are added in order. Here thread
+      // q = 2 w + h holds the 16-byte unit at column (5 w + f) 16 + 8 h of
+      // every f, i.e. the columns of lane groups 2 h and 2 h + 1.
+      static_assert(BT * 16 == 64 * NW && XS == 1 && CT == 5, "row normalisation: 16 threads per 640-wide row");
       const int r = tid >> 4, q = tid & 15;
-      const int slot = (q ^ (r & 15)) << 3;
+      const int w8 = q >> 1, hh = q & 1;
       u4_t hs[CT];
-      float ss = 0.0f;
+      int slot[CT], colf[CT];
+      float pa = 0.0f, pb = 0.0f;
 #pragma unroll
-      for (int c = 0; c < CT; ++c) {
-        const h8_t o8 = *reinterpret_cast<const h8_t*>(xs_lds + c * PLANE + r * KC + slot);
-        const h8_t r8 = *reinterpret_cast<const h8_t*>(xs_lds + (CT + c) * PLANE + r * KC + slot);
+      for (int f = 0; f < CT; ++f) {
+        colf[f] = (5 * w8 + f) * 16 + 8 * hh;
+        slot[f] = (colf[f] >> 7) * PLANE + r * KC + ((((colf[f] & 127) >> 3) ^ (r & 15)) << 3);
+        const h8_t o8 = *reinterpret_cast<const h8_t*>(xs_lds + slot[f]);
+        const h8_t r8 = *reinterpret_cast<const h8_t*>(xs_lds + CT * PLANE + slot[f]);
         float sv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          sv[i] = (float)o8[i] + (float)r8[i];
-          ss += sv[i] * sv[i];
-        }
-        const u2_t lo = to_f16x4(sv), hi = to_f16x4(sv + 4);
-        hs[c] = u4_t{lo.x, lo.y, hi.x, hi.y};
-      }
+        for (int i = 0; i < 8; ++i) sv[i] = (float)o8[i] + (float)r8[i];
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
-      const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)(CT * KC)) + p.nrm_eps);
+        for (int i = 0; i < 4; ++i) pa = fmaf(sv[i], sv[i], pa);
+#pragma unroll
+        for (int i = 4; i < 8; ++i) pb = fmaf(sv[i], sv[i], pb);
+        const u2_t lo = to_f16x4_native(sv), hi = to_f16x4_native(sv + 4);
+        hs[f] = u4_t{lo.x, lo.y, hi.x, hi.y};
+      }
+      float qv = pa + pb;
+      qv += __shfl_xor(qv, 1, 64);
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) tot += __shfl(qv, (lane & ~15) + 2 * w, 64);
+      const float inv_rms = 1.0f / sqrtf(tot * (1.0f / (float)(CT * KC)) + p.nrm_eps);
       const bool store = r < rows;
       const size_t orow = (size_t)(row0 + r) * (CT * KC);
       __syncthreads();  // every thread has read its o and residual units
 #pragma unroll
-      for (int c = 0; c < CT; ++c) {
-        const int col = c * KC + q * 8;
-        const u4_t gw = *reinterpret_cast<const u4_t*>(p.nrm_gamma + col);
-        const h8_t h8 = __builtin_bit_cast(h8_t, hs[c]);
+      for (int f = 0; f < CT; ++f) {
+        const u4_t gw = *reinterpret_cast<const u4_t*>(p.nrm_gamma + colf[f]);
+        const h8_t h8 = __builtin_bit_cast(h8_t, hs[f]);
         const h8_t g8 = __builtin_bit_cast(h8_t, gw);
         float y[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = (float)h8[i] * inv_rms * (float)g8[i];
-        const u2_t lo = to_f16x4(y), hi = to_f16x4(y + 4);
+        const u2_t lo = to_f16x4_native(y), hi = to_f16x4_native(y + 4);
         const u4_t xv = u4_t{lo.x, lo.y, hi.x, hi.y};
-        *reinterpret_cast<u4_t*>(xs_lds + c * PLANE + r * KC + slot) = xv;
+        *reinterpret_cast<u4_t*>(xs_lds + slot[f]) = xv;
         if (store) {
-          *reinterpret_cast<u4_t*>(p.nrm_h + orow + col) = hs[c];
-          *reinterpret_cast<u4_t*>(p.nrm_xn + orow + col) = xv;
+          *reinterpret_cast<u4_t*>(p.nrm_h + orow + colf[f]) = hs[f];
+          *reinterpret_cast<u4_t*>(p.nrm_xn + orow + colf[f]) = xv;
         }
       }
       __syncthreads();
@@ -729,7 +743,9 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   PF_CHECK(a.ldx % 8 == 0, "gemm_w4: activation row stride must allow 16-byte loads");
   PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
            "gemm_w4: activations and weights must be 16-byte aligned");
-  PF_CHECK((long)a.M * a.ldx < (1L << 31) || grouped, "gemm_w4: activation offsets exceed 32 bits");
+  // activation rows are addressed with 32-bit element offsets (grouped: a.M
+  // slots bound every row the tile list or the row map can name)
+  PF_CHECK((long)a.M * a.ldx < (1L << 31), "gemm_w4: activation offsets exceed 32 bits");
   if (xk == XKind::SPLIT)
     PF_CHECK(a.x_lo && (reinterpret_cast<uintptr_t>(a.x_lo) & 15) == 0, "gemm_w4: SPLIT needs an aligned lo plane");
   if (epi == Epi::SWIGLU_SPLIT || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_w4: SwiGLU needs N % 4 == 0");
@@ -873,11 +889,13 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   f4_t acc[WF][TJ];
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
+    // the bias widens as k_gemm_w4 widens it (the two O forms agree bit for bit)
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
     if (p.bias) {
-      const h4_t bh = __builtin_bit_cast(h4_t, *reinterpret_cast<const u2_t*>(p.bias + ncol[f]));
+      const u2_t bw = *reinterpret_cast<const u2_t*>(p.bias + ncol[f]);
+      const uint32_t bwv[2] = {bw.x, bw.y};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bv[r] = (float)bh[r];
+      for (int r = 0; r < 4; ++r) bv[r] = wasm_h2f((uint16_t)(bwv[r >> 1] >> (16 * (r & 1))));
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};

@@ -139,6 +139,15 @@ struct GemmArgs {
 void gemm_int4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool grouped, int tile_t,
                const char* prof_name);
 
+// Tile of the grouped expert GEMMs for M tokens routed to topk of experts:
+// t tokens per tile (128, 64 or 16; also the routing plan's tile) and wf
+// 16-row weight fragments per wave (gemm_w4). The forward and the moe_ffn
+// named kernel choose it the same way.
+struct ExpertTile {
+  int t, wf;
+};
+ExpertTile expert_tile(int M, int topk, int experts, bool fp16, int D, int F);
+
 // Scale-folded int4 GEMM (gemm_w4.hip): weights prepared by w4_prepare;
 // K % 128 == 0. tile_t x wf selects the tile (BT tokens x 64*wf rows):
 // (128, 4), (128, 2), (64, 5), (64, 1), and the small-M tiles (16, 1) and

@@ -337,6 +337,45 @@ static std::vector<KernelEntry>& registry() {
                  a.K = K;
                  gemm_w4(b, a, XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, tile_t, wf, "matmul_int4_w4");
                }});
+  // matmul_int4_w4_topk: the router GEMM of the fp16 forward with its top-4 + softmax epilogue
+  // (gemm_w4 F32_TOPK; N == 128 experts, k == 4). push {T, N, K, tile_t} (tile_t 128 or 16, the two
+  // row tiles the forward selects by row count); bindings [x fp16, w, scales, zp, bias, logits f32 [T][N],
+  // routing_idx i32 [T][4], routing_w f32 [T][4]]
+  r.push_back({"matmul_int4_w4_topk", 8, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), N = (int)pu(p, 1), K = (int)pu(p, 2), tile_t = (int)pu(p, 3);
+                 PF_CHECK(N == 128 && K % 128 == 0 && (tile_t == 128 || tile_t == 16),
+                          "matmul_int4_w4_topk: N must be 128, K a multiple of 128 and tile_t 128 or 16");
+                 const int nb = K / 32;
+                 need(bs, 0, (size_t)T * K * 2, "matmul_int4_w4_topk");
+                 need(bs, 1, (size_t)N * K / 2, "matmul_int4_w4_topk");
+                 need(bs, 2, (size_t)N * nb * 2, "matmul_int4_w4_topk");
+                 need(bs, 3, (size_t)N * ((nb + 1) / 2), "matmul_int4_w4_topk");
+                 need(bs, 4, (size_t)N * 2, "matmul_int4_w4_topk");
+                 need(bs, 5, (size_t)T * N * 4, "matmul_int4_w4_topk");
+                 need(bs, 6, (size_t)T * 4 * 4, "matmul_int4_w4_topk");
+                 need(bs, 7, (size_t)T * 4 * 4, "matmul_int4_w4_topk");
+                 const size_t wbytes = ((size_t)N * K / 2 + 255) & ~(size_t)255;
+                 char* prep = static_cast<char*>(backend_scratch(b, wbytes + (size_t)N * nb * 4));
+                 uint32_t* w4 = reinterpret_cast<uint32_t*>(prep);
+                 uint32_t* sz = reinterpret_cast<uint32_t*>(prep + wbytes);
+                 w4_prepare(b, bp<uint8_t>(bs, 1), bp<uint16_t>(bs, 2), bp<uint8_t>(bs, 3), w4, sz, N, K);
+                 GemmArgs a;
+                 a.x = bs[0]->ptr;
+                 a.ldx = K;
+                 a.w = reinterpret_cast<const uint8_t*>(w4);
+                 a.wsz = sz;
+                 a.bias = bp<uint16_t>(bs, 4);
+                 a.out = bs[5]->ptr;
+                 a.ldo = N;
+                 a.M = T;
+                 a.N = N;
+                 a.K = K;
+                 a.topk_idx = bp<int32_t>(bs, 6);
+                 a.topk_w = bp<float>(bs, 7);
+                 a.topk_k = 4;
+                 a.topk_wscale = 1.0f;
+                 gemm_w4(b, a, XKind::F16, Epi::F32_TOPK, false, tile_t, 2, "matmul_int4_w4_topk");
+               }});
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), K = (int)pu(p, 1), E = (int)pu(p, 2), tt = (int)pu(p, 3);
@@ -356,26 +395,46 @@ static std::vector<KernelEntry>& registry() {
                  moe_route(b, bp<int32_t>(bs, 0), T, K, E, m);
                }});
   // moe_ffn: one MoE FFN layer.
-  // push {T, D, E, K, dff, router_int4 (0: fp16 router W [D][E]; 1: MatMulNBits router), x_f32, 0}
+  // push {T, D, E, K, dff, router_int4 (0: fp16 router W [D][E]; 1: MatMulNBits router), x_f32, precision}
+  // precision 0: the split numerics (gemm_int4, f32 activations as hi/lo planes, per-block f32 scaling);
+  // precision 1: the forward's fp16 numerics (gemm_w4 grouped SwiGLU and down kernels on scale-folded
+  // weights, fp16 SwiGLU output), with the forward's expert tile choice (expert_tile).
   // bindings [x, router_w, router_scales|-, router_zp|-, router_bias, gu.int4, gu.scales, gu.zp, gu.bias,
   //           dn.int4, dn.scales, dn.zp, dn.bias, out fp16 [T][D], routing_idx [T][K], routing_w [T][K]]
   r.push_back({"moe_ffn", 16, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), D = (int)pu(p, 1), E = (int)pu(p, 2), K = (int)pu(p, 3);
                  const int F = (int)pu(p, 4);
                  const bool rint4 = pu(p, 5) != 0, xf32 = pu(p, 6) != 0;
+                 const uint32_t prec = pu(p, 7);
+                 PF_CHECK(prec <= 1, "moe_ffn: precision must be 0 (split) or 1 (fp16)");
+                 const bool f16 = prec == 1;
+                 PF_CHECK(T >= 1 && E >= K && K >= 1 && K <= 8, "moe_ffn: bad T / E / K");
                  PF_CHECK(D % 32 == 0 && F % 32 == 0, "moe_ffn: D and dff must be multiples of 32");
+                 if (f16)
+                   PF_CHECK(!xf32 && D % 128 == 0 && F % 128 == 0,
+                            "moe_ffn: the fp16 numerics take fp16 activations and D, dff multiples of 128");
                  need(bs, 0, (size_t)T * D * (xf32 ? 4 : 2), "moe_ffn");
                  need(bs, 13, (size_t)T * D * 2, "moe_ffn");
                  need(bs, 14, (size_t)T * K * 4, "moe_ffn");
                  need(bs, 15, (size_t)T * K * 4, "moe_ffn");
                  need(bs, 5, (size_t)E * 2 * F * D / 2, "moe_ffn");
+                 need(bs, 6, (size_t)E * 2 * F * (D / 32) * 2, "moe_ffn");
+                 need(bs, 7, (size_t)E * 2 * F * ((D / 32 + 1) / 2), "moe_ffn");
+                 need(bs, 8, (size_t)E * 2 * F * 2, "moe_ffn");
                  need(bs, 9, (size_t)E * D * F / 2, "moe_ffn");
-                 const int tt = (T * K / E >= 256) ? 128 : 64;
+                 need(bs, 10, (size_t)E * D * (F / 32) * 2, "moe_ffn");
+                 need(bs, 11, (size_t)E * D * ((F / 32 + 1) / 2), "moe_ffn");
+                 need(bs, 12, (size_t)E * D * 2, "moe_ffn");
+                 const ExpertTile et = expert_tile(T, K, E, f16, D, F);
+                 const int tt = et.t;
                  const size_t S = (size_t)T * K;
                  auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
                  const size_t plan_b = moe_plan_bytes(T, K, E, tt);
+                 const size_t gu_w = al((size_t)E * 2 * F * D / 2), gu_s = al((size_t)E * 2 * F * (D / 32) * 4);
+                 const size_t dn_w = al((size_t)E * D * F / 2), dn_s = al((size_t)E * D * (F / 32) * 4);
                  const size_t bytes = al((size_t)T * E * 4) + 2 * al(S * F * 2) + al(S * D * 4) +
-                                      2 * al((size_t)T * D * 2) + al((size_t)T * D * 2) + plan_b;
+                                      2 * al((size_t)T * D * 2) + al((size_t)T * D * 2) + plan_b +
+                                      (f16 ? gu_w + gu_s + dn_w + dn_s : 0);
                  char* s = static_cast<char*>(backend_scratch(b, bytes));
                  float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
                  uint16_t* glu_hi = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
@@ -384,7 +443,7 @@ static std::vector<KernelEntry>& registry() {
                  uint16_t* x_hi = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  uint16_t* x_lo = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
-                 MoePlan m = moe_plan_carve(s, T, K, E, tt);
+                 MoePlan m = moe_plan_carve(s, T, K, E, tt); s += plan_b;
                  // activations: f32 input -> hi/lo planes; an fp16 input is exact as one plane
                  const XKind xk = xf32 ? XKind::SPLIT : XKind::F16;
                  const void* xin = bs[0]->ptr;
@@ -415,7 +474,6 @@ static std::vector<KernelEntry>& registry() {
                  g.wz_gs = (size_t)2 * F * ((D / 32 + 1) / 2); g.bias_gs = (size_t)2 * F;
                  g.out = glu_hi; g.out_lo = glu_lo; g.ldo = F; g.M = (int)S; g.N = 2 * F; g.K = D;
                  g.tiles = m.tiles; g.num_tiles = m.num_tiles; g.max_tiles = m.max_tiles;
-                 gemm_int4(b, g, xk, Epi::SWIGLU_SPLIT, true, tt, "moe_gate_up");
                  GemmArgs d;
                  d.x = glu_hi; d.x_lo = glu_lo; d.ldx = F;
                  d.w = bp<uint8_t>(bs, 9); d.ws = bp<uint16_t>(bs, 10); d.wz = bp<uint8_t>(bs, 11);
@@ -424,7 +482,24 @@ static std::vector<KernelEntry>& registry() {
                  d.wz_gs = (size_t)D * ((F / 32 + 1) / 2); d.bias_gs = (size_t)D;
                  d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
                  d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
-                 gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "moe_down");
+                 if (f16) {
+                   // the forward's path: weights repacked with the block scale folded in
+                   uint32_t* guw = reinterpret_cast<uint32_t*>(s); s += gu_w;
+                   uint32_t* gus = reinterpret_cast<uint32_t*>(s); s += gu_s;
+                   uint32_t* dnw = reinterpret_cast<uint32_t*>(s); s += dn_w;
+                   uint32_t* dns = reinterpret_cast<uint32_t*>(s); s += dn_s;
+                   w4_prepare(b, g.w, g.ws, g.wz, guw, gus, E * 2 * F, D);
+                   w4_prepare(b, d.w, d.ws, d.wz, dnw, dns, E * D, F);
+                   g.w = reinterpret_cast<const uint8_t*>(guw); g.wsz = gus; g.wsz_gs = (size_t)2 * F * (D / 32);
+                   g.out_lo = nullptr;
+                   gemm_w4(b, g, XKind::F16, Epi::SWIGLU_F16, true, et.t, et.wf, "moe_gate_up");
+                   d.x_lo = nullptr;
+                   d.w = reinterpret_cast<const uint8_t*>(dnw); d.wsz = dns; d.wsz_gs = (size_t)D * (F / 32);
+                   gemm_w4(b, d, XKind::F16, Epi::F32, true, et.t, et.wf, "moe_down");
+                 } else {
+                   gemm_int4(b, g, xk, Epi::SWIGLU_SPLIT, true, tt, "moe_gate_up");
+                   gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "moe_down");
+                 }
                  // out = fp16(sum_k w_k y_k) (zero residual -> h_out holds the MoE output)
                  zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
                  moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, zero_res, nullptr,

@@ -148,6 +148,15 @@ def make_model_weights(cfg: ModelConfig = PF_CONFIG, seed: int = 20260101, *, nu
     return w
 
 
+def zipf_router(seed: int, d: int, e: int, s: float = 1.1, strength: float = 0.35):
+    """BASELINE config 3's router: fp16 W [d][e] ~ N(0, 0.02) and an fp16
+    bias of -s * strength * ln(rank) (rank = expert id + 1), which skews the
+    realised top-k load towards Zipf(s). Returns (W bits [d][e], bias bits [e])."""
+    w = to_fp16_bits(normal(seed, d * e, 0, 0.02)).reshape(d, e)
+    bias = to_fp16_bits(s * -np.log(np.arange(1, e + 1)) * strength)
+    return w, bias
+
+
 def token_ids(seed: int, n: int, vocab: int = PF_CONFIG.vocab_size) -> np.ndarray:
     """Token ids uniform over [0, vocab) (BASELINE configs 2 and 5)."""
     return (u64(seed, n) % np.uint64(vocab)).astype(np.int32)
