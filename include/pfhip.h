@@ -146,6 +146,23 @@ int pfhip_model_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
  * mask may be NULL. Returns after the forward has completed. */
 int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* mask, uint32_t batch,
                                uint32_t seq_len, pfhip_buffer* logits, char* err, size_t err_cap);
+/* Allocation-free variant of pfhip_model_forward_device. It has no
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, kernels and results as
+ * pfhip_model_forward_device, but the forward's scratch (activations, routing
+ * plan) is a fixed device array of PFHIP_NOALLOC_SCRATCH_MIB MiB per GPU,
+ * held from the library's set-up on that GPU (pfhip_create_backend) until the
+ * process ends, and nothing is allocated: batch * seq_len must fit that array
+ * (one 2048-token sequence of the privacy-filter model does) and seq_len must
+ * not exceed the RoPE tables already built (pfhip_model_finalize builds them
+ * for 2048 positions; a longer pfhip_model_forward_device call grows them).
+ * Larger requests fail with an error before any work. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (from several
+ * threads, backends or models) race. Debug taps are not recorded. */
+#define PFHIP_NOALLOC_SCRATCH_MIB 80
+int pfhip_model_forward_device_noalloc(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* mask, uint32_t batch,
+                                       uint32_t seq_len, pfhip_buffer* logits, char* err, size_t err_cap);
 /* Debug taps of the last forward (for parity tests): copies a named
  * intermediate ("h.L" residual after layer L, "logits16") to the host. */
 int pfhip_model_read_tap(pfhip_model* m, const char* name, void* dst, size_t n, char* err, size_t err_cap);

@@ -74,6 +74,8 @@ EXPORTS = [
                                       C.c_char_p, C.c_size_t]),
     ("pfhip_model_forward_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
                                              C.c_void_p, C.c_char_p, C.c_size_t]),
+    ("pfhip_model_forward_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
+                                                     C.c_void_p, C.c_char_p, C.c_size_t]),
     ("pfhip_model_read_tap", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
     ("pfhip_model_enable_taps", C.c_int, [C.c_void_p, C.c_int]),
     ("pfhip_rope_tables", C.c_int, [C.POINTER(ModelConfigC), C.c_uint32, C.c_void_p, C.c_void_p]),
@@ -245,6 +247,14 @@ class Model:
         e = _err()
         _check(lib().pfhip_model_forward_device(self.handle, ids.handle, mask.handle if mask else None, batch, seq_len,
                                                 logits.handle, e, ERR_CAP), e, "forward_device")
+
+    def forward_device_noalloc(self, ids: Buffer, mask: Buffer | None, batch: int, seq_len: int, logits: Buffer):
+        """pfhip_model_forward_device_noalloc: the same forward with its scratch
+        in the library's fixed per-GPU array; allocates nothing."""
+        e = _err()
+        _check(lib().pfhip_model_forward_device_noalloc(self.handle, ids.handle, mask.handle if mask else None, batch,
+                                                        seq_len, logits.handle, e, ERR_CAP), e,
+               "forward_device_noalloc")
 
     def enable_taps(self, on: bool = True):
         lib().pfhip_model_enable_taps(self.handle, int(on))

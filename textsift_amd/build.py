@@ -18,7 +18,8 @@ BUILD = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libpfhip.so")
 
-SOURCES = ["gemm_int4.hip", "gemm_w4.hip", "attention.hip", "kernels_misc.hip", "runtime.cpp", "forward.cpp", "viterbi.cpp"]
+SOURCES = ["gemm_int4.hip", "gemm_w4.hip", "attention.hip", "kernels_misc.hip", "noalloc.hip", "runtime.cpp", "forward.cpp",
+           "viterbi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -102,8 +102,9 @@ struct pfhip_model {
   pfhip_buffer* ids_buf = nullptr;
   pfhip_buffer* mask_buf = nullptr;
   pfhip_buffer* logits_buf = nullptr;
-  // debug taps
+  // debug taps (not recorded by the allocation-free entry)
   bool taps = false;
+  bool in_noalloc = false;
   std::map<std::string, std::vector<uint8_t>> tap;
 };
 
@@ -290,14 +291,48 @@ void cast_f16_f32_ieee(pfhip_backend* b, const uint16_t* s, float* d, size_t n);
 }
 
 static void record_tap(pfhip_model* m, const std::string& name, const void* dev, size_t bytes) {
-  if (!m->taps) return;
+  if (!m->taps || m->in_noalloc) return;
   std::vector<uint8_t>& v = m->tap[name];
   v.resize(bytes);
   PF_HIP(hipMemcpyAsync(v.data(), dev, bytes, hipMemcpyDeviceToHost, m->b->stream));
   PF_HIP(hipStreamSynchronize(m->b->stream));
 }
 
-static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask, int B, int T, float* logits_out) {
+// Host-built YARN tables for T positions, replacing smaller ones.
+static void ensure_rope(pfhip_model* m, int T) {
+  pfhip_backend* b = m->b;
+  std::vector<uint16_t> cs, sn;
+  build_rope_tables(m->cfg, T, cs, sn);
+  if (m->rope_cos) {
+    PF_HIP(hipStreamSynchronize(b->stream));
+    hipFree(m->rope_cos);
+    hipFree(m->rope_sin);
+    hipFree(m->rope_pairs);
+    m->rope_cos = m->rope_sin = nullptr;
+    m->rope_pairs = nullptr;
+    m->rope_T = 0;
+  }
+  std::vector<float> csf(cs.size()), snf(sn.size());
+  std::vector<uint16_t> pairs(2 * cs.size());
+  for (size_t i = 0; i < cs.size(); ++i) {
+    csf[i] = wasm_h2f_host(cs[i]);
+    snf[i] = wasm_h2f_host(sn[i]);
+    pairs[2 * i] = cs[i];
+    pairs[2 * i + 1] = sn[i];
+  }
+  PF_HIP(hipMalloc(&m->rope_cos, csf.size() * 4));
+  PF_HIP(hipMalloc(&m->rope_sin, snf.size() * 4));
+  PF_HIP(hipMalloc(&m->rope_pairs, pairs.size() * 2));
+  PF_HIP(hipMemcpy(m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice));
+  PF_HIP(hipMemcpy(m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice));
+  PF_HIP(hipMemcpy(m->rope_pairs, pairs.data(), pairs.size() * 2, hipMemcpyHostToDevice));
+  m->rope_T = T;
+}
+
+// fixed_scratch: the allocation-free entry's scratch (nothing is allocated
+// and no taps are recorded); NULL: the model's own, grown as needed.
+static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask, int B, int T, float* logits_out,
+                        void* fixed_scratch = nullptr) {
   pfhip_backend* b = m->b;
   const pfhip_model_config& c = m->cfg;
   const int M = B * T;
@@ -309,7 +344,13 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   // scratch (the layout's size is not monotonic in M: the expert tile list
   // of a smaller M on a smaller tile can be longer)
   const size_t bytes = scratch_layout(c, M, nullptr, nullptr);
-  if (bytes > m->scratch_bytes) {
+  void* base = fixed_scratch;
+  if (fixed_scratch) {
+    PF_CHECK(bytes <= NOALLOC_SCRATCH_BYTES, "batch * seq_len = " + std::to_string(M) + " needs " +
+                                                 std::to_string(bytes) + " bytes of scratch, more than the " +
+                                                 std::to_string(NOALLOC_SCRATCH_BYTES) +
+                                                 " of the allocation-free forward");
+  } else if (bytes > m->scratch_bytes) {
     if (m->scratch) {
       PF_HIP(hipStreamSynchronize(b->stream));
       PF_HIP(hipFree(m->scratch));
@@ -318,37 +359,17 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     PF_HIP(hipMalloc(&m->scratch, bytes));
     m->scratch_bytes = bytes;
   }
+  if (!base) base = m->scratch;
   Scr s;
-  scratch_layout(c, M, &s, m->scratch);
+  scratch_layout(c, M, &s, base);
   MoePlan plan = moe_plan_carve(s.plan, M, K, E, tt);
 
-  // RoPE tables (host-built, cached per sequence length)
-  if (m->rope_T != T) {
-    std::vector<uint16_t> cs, sn;
-    build_rope_tables(c, T, cs, sn);
-    if (m->rope_cos) {
-      PF_HIP(hipStreamSynchronize(b->stream));
-      hipFree(m->rope_cos);
-      hipFree(m->rope_sin);
-      hipFree(m->rope_pairs);
-      m->rope_cos = m->rope_sin = nullptr;
-      m->rope_pairs = nullptr;
-    }
-    std::vector<float> csf(cs.size()), snf(sn.size());
-    std::vector<uint16_t> pairs(2 * cs.size());
-    for (size_t i = 0; i < cs.size(); ++i) {
-      csf[i] = wasm_h2f_host(cs[i]);
-      snf[i] = wasm_h2f_host(sn[i]);
-      pairs[2 * i] = cs[i];
-      pairs[2 * i + 1] = sn[i];
-    }
-    PF_HIP(hipMalloc(&m->rope_cos, csf.size() * 4));
-    PF_HIP(hipMalloc(&m->rope_sin, snf.size() * 4));
-    PF_HIP(hipMalloc(&m->rope_pairs, pairs.size() * 2));
-    PF_HIP(hipMemcpy(m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice));
-    PF_HIP(hipMemcpy(m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice));
-    PF_HIP(hipMemcpy(m->rope_pairs, pairs.data(), pairs.size() * 2, hipMemcpyHostToDevice));
-    m->rope_T = T;
+  // RoPE tables: built on the host for at least T positions (row t depends
+  // on t alone, so tables built for more positions serve any shorter T)
+  if (m->rope_T < T) {
+    PF_CHECK(!fixed_scratch, "seq_len exceeds the RoPE tables already built (the allocation-free forward "
+                             "cannot build longer ones)");
+    ensure_rope(m, T);
   }
 
   const bool f16 = c.precision == PFHIP_PRECISION_FP16;
@@ -650,6 +671,8 @@ int pfhip_model_finalize(pfhip_model* m, char* err, size_t cap) {
       m->layers.push_back(L);
     }
     if (c.precision == PFHIP_PRECISION_FP16) m->score4 = prepare_w4(m, qw(m, "score"), c.classes, D);
+    // RoPE tables for one reference chunk (privacy-filter.ts:559: 2048 tokens)
+    if (m->rope_T < 2048) ensure_rope(m, 2048);
     PF_HIP(hipStreamSynchronize(m->b->stream));
     m->finalized = true;
     return 0;
@@ -681,6 +704,38 @@ int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* 
     PF_HIP(hipSetDevice(m->b->device));
     run_forward(m, static_cast<const int32_t*>(ids->ptr), mask ? static_cast<const uint8_t*>(mask->ptr) : nullptr,
                 (int)batch, (int)seq_len, static_cast<float*>(logits->ptr));
+    PF_HIP(hipStreamSynchronize(m->b->stream));
+    prof_flush(m->b);
+    return 0;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return -1;
+  }
+}
+
+int pfhip_model_forward_device_noalloc(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* mask, uint32_t batch,
+                                       uint32_t seq_len, pfhip_buffer* logits, char* err, size_t cap) {
+  try {
+    PF_CHECK(m && ids && logits, "null argument");
+    PF_CHECK(batch >= 1 && seq_len >= 1, "batch and seq_len must be positive");
+    const size_t M = (size_t)batch * seq_len;
+    PF_CHECK(M <= (1u << 22), "batch * seq_len too large");
+    check_row_limits(m->cfg, M);
+    PF_CHECK(m->finalized, "call pfhip_model_finalize() first");
+    PF_CHECK(ids->size >= M * 4, "ids buffer too small");
+    PF_CHECK(!mask || mask->size >= M, "mask buffer too small");
+    PF_CHECK(logits->size >= M * m->cfg.classes * 4, "logits buffer too small");
+    PF_HIP(hipSetDevice(m->b->device));
+    void* fixed = noalloc_scratch(m->b->device);  // looked up at backend creation; no allocation here
+    m->in_noalloc = true;
+    try {
+      run_forward(m, static_cast<const int32_t*>(ids->ptr), mask ? static_cast<const uint8_t*>(mask->ptr) : nullptr,
+                  (int)batch, (int)seq_len, static_cast<float*>(logits->ptr), fixed);
+    } catch (...) {
+      m->in_noalloc = false;
+      throw;
+    }
+    m->in_noalloc = false;
     PF_HIP(hipStreamSynchronize(m->b->stream));
     prof_flush(m->b);
     return 0;

@@ -241,6 +241,12 @@ void qmoe_down_scatter_ref(pfhip_backend* b, const float* glu, const int32_t* ri
                            const uint8_t* w, const uint16_t* ws, const uint8_t* wz, const uint16_t* bias, float* acc,
                            int T, int K, int N, int D);
 
+// Fixed device scratch of the allocation-free forward entry (noalloc.hip):
+// PFHIP_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. Returns
+// its address on `device` (looked up once per device, with that device current).
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)PFHIP_NOALLOC_SCRATCH_MIB << 20;
+void* noalloc_scratch(int device);
+
 // Plain device copy of `bytes` (multiple of 16, 16-byte aligned).
 void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes);
 

@@ -569,6 +569,9 @@ pfhip_backend* pfhip_create_backend(int device, char* err, size_t cap) {
     b->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
     b->num_cus = prop.multiProcessorCount;
     PF_HIP(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
+    // set-up of the allocation-free forward's fixed scratch on this device
+    // (its address is looked up once per device, with the device current)
+    noalloc_scratch(device);
     return b;
   } catch (const std::exception& ex) {
     set_err(err, cap, ex.what());
