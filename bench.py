@@ -62,8 +62,25 @@ KERNEL_LABELS = [
     ("moe_scatter", ("k_moe_scatter",)),
     ("embed_lookup_int4", ("k_embed",)),
     ("rms_norm", ("k_rms_norm",)),
+    ("copy_lds", ("k_copy16_lds",)),
+    ("gather16", ("k_gather16",)),
     ("copy", ("k_copy16",)),
 ]
+CALIBRATION = ("copy", "copy_lds", "gather16")
+
+
+def short_symbol(sym):
+    """A kernel symbol without namespace qualifiers and parameter list."""
+    s = sym.replace("void ", "").replace("pf::(anonymous namespace)::", "").replace("pf::", "")
+    depth = 0
+    for i, ch in enumerate(s):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return s[:i]
+    return s
 
 
 LABELS = list(dict.fromkeys(lab for lab, _ in KERNEL_LABELS))  # unique, in order
@@ -98,29 +115,43 @@ def read_counters(path, counter):
     return out
 
 
-def traffic_report(fetch_csv, write_csv, copy_mb):
+def traffic_report(fetch_csv, write_csv, copy_mb, raw=False):
     """Markdown summary: per kernel, FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch) scaled by what the counters read for a plain copy of copy_mb MiB."""
+    dispatch) scaled by what the counters read for calibration workloads of
+    known size run in the same process (--copy-calibration-mb): a plain copy
+    of copy_mb MiB (the factor applied), the same copy with HBM -> LDS loads,
+    and a gather of copy_mb MiB in scattered 16-byte units (reported, so a
+    reader sees whether the factor depends on the load form).
+    raw: kernels by their symbols instead of the forward's launch names."""
     fetch = read_counters(fetch_csv, "FETCH_SIZE")
     write = read_counters(write_csv, "WRITE_SIZE")
     expect_kib = copy_mb * 1024.0
+    def key(name):
+        lab = label_of(name)
+        if lab in CALIBRATION or not raw:
+            return lab
+        return short_symbol(name)
     def per_label(d):
         acc = {}
         for name, v in d.values():
-            lab = label_of(name)
+            lab = key(name)
             if lab:
                 acc.setdefault(lab, []).append(v)
         return acc
     fl, wl = per_label(fetch), per_label(write)
-    copy_f = max(fl.get("copy", [0.0]))
-    copy_w = max(wl.get("copy", [0.0]))
-    kf = copy_f / expect_kib if copy_f else None
-    kw = copy_w / expect_kib if copy_w else None
+    # calibration: bytes each workload moves (read, write) in KiB
+    known = {"copy": (expect_kib, expect_kib), "copy_lds": (expect_kib, expect_kib),
+             "gather16": (expect_kib * 1.25, expect_kib)}  # gather reads a 4-byte index per 16-byte unit
+    factors = {}
+    for c in CALIBRATION:
+        if c in fl and c in wl:
+            factors[c] = (max(fl[c]) / known[c][0], max(wl[c]) / known[c][1])
+    kf, kw = factors.get("copy", (None, None))
     lines = ["| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/launch |",
              "|---|---|---|---|---|"]
     summary = {}
-    for lab in LABELS:
-        if lab == "copy" or lab not in fl or lab not in wl:
+    for lab in sorted(set(fl) & set(wl), key=lambda x: (LABELS.index(x) if x in LABELS else len(LABELS), x)):
+        if lab in CALIBRATION:
             continue
         f = sum(fl[lab]) / len(fl[lab])
         w = sum(wl[lab]) / len(wl[lab])
@@ -128,11 +159,26 @@ def traffic_report(fetch_csv, write_csv, copy_mb):
         summary[lab] = hbm
         lines.append(f"| {lab} | {len(fl[lab])} | {f:.1f} | {w:.1f} | {hbm:.4g} |" if hbm else
                      f"| {lab} | {len(fl[lab])} | {f:.1f} | {w:.1f} | - |")
-    head = [f"calibration copy of {copy_mb} MiB: FETCH_SIZE {copy_f:.1f} KiB (factor {kf:.4f}), "
-            f"WRITE_SIZE {copy_w:.1f} KiB (factor {kw:.4f}); HBM bytes/launch = (FETCH/f_fetch + WRITE/f_write) * 1024",
-            ""] if kf and kw else ["no calibration copy found", ""]
+    head = []
+    for c, (a, b) in factors.items():
+        head.append(f"calibration {c} of {copy_mb} MiB: FETCH_SIZE factor {a:.4f}, WRITE_SIZE factor {b:.4f}")
+    head += ["HBM bytes/launch = (FETCH / copy FETCH factor + WRITE / copy WRITE factor) * 1024", ""] if kf and kw \
+        else ["no calibration copy found", ""]
     tail = [""] + [f"hbm_bytes_per_launch {lab}: {int(v)}" for lab, v in summary.items() if v]
     return "\n".join(head + lines + tail)
+
+
+def run_calibration(be, mib):
+    """The counters' calibration workloads, copy_mb MiB each (see traffic_report)."""
+    n = mib << 20
+    src, dst = be.buffer(nbytes=n), be.buffer(nbytes=n)
+    be.dispatch("copy16", [src, dst], np.array([n], np.uint32))
+    be.dispatch("copy16_lds", [src, dst], np.array([n], np.uint32))
+    units = n // 16
+    idx = be.buffer(np.random.default_rng(0).integers(0, units, units).astype(np.int32))
+    be.dispatch("gather16", [src, idx, dst], np.array([units, units], np.uint32))
+    for b in (src, dst, idx):
+        b.release()
 
 
 SQ_PASS1 = "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_WAIT_INST_ANY SQ_WAIT_ANY " \
@@ -310,15 +356,360 @@ def cpu_threads():
     return max(1, min(n, 16))
 
 
+# ---------------------------------------------------------------- per-config measurement
+
+CACHE_COLD_BYTES = 512 << 20   # rotate inputs over at least this much memory: 2x the 256 MB MALL
+
+
+def host_cpu():
+    """(threads this process may use, CPU model name) of the host."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return n, model
+
+
+def ref_default_threads(n):
+    """The reference's WASM worker count for a host of n cores,
+    max(2, min(6, cores - 1)) (browser/backends/wasm.ts:659-661)."""
+    return max(2, min(6, n - 1))
+
+
+def timed_threads(fn, n_threads, reps=3):
+    """Median wall time of fn(n_threads) over reps runs (after one warmup)."""
+    fn(n_threads)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn(n_threads)
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def sliced(fn, total, n_threads):
+    """Runs fn(lo, hi) over n_threads contiguous slices of range(total) on host
+    threads (the oracle's C code releases the GIL), as the reference's MtPool
+    partitions its work (T-slices for GEMMs, H_q-slices for attention)."""
+    from concurrent.futures import ThreadPoolExecutor
+    n = max(1, min(n_threads, total))
+    bounds = [(total * i // n, total * (i + 1) // n) for i in range(n)]
+    with ThreadPoolExecutor(max_workers=n) as ex:
+        list(ex.map(lambda b: fn(*b), bounds))
+
+
+def cpu_baseline_both(work_fn, units, unit, sample):
+    """The oracle timed at the reference's default thread count and at all host
+    cores (capped at 16, the box's CPU share): {value, unit, cores, ...}."""
+    n, model = host_cpu()
+    allc = max(1, min(n, 16))
+    refc = ref_default_threads(n)
+    t_all = timed_threads(work_fn, allc)
+    t_ref = t_all if refc == allc else timed_threads(work_fn, refc)
+    return {"value": round(units / t_all, 3), "unit": unit, "cores": allc, "kind": "port",
+            "sample": sample, "host_nproc": n, "cpu_model": model,
+            "reference_default_threads": {"cores": refc, "value": round(units / t_ref, 3)}}
+
+
+def time_dispatch(be, name, make_bindings, push, copies, reps):
+    """Median device time (HIP events around the whole named dispatch, on the
+    backend's stream) of `reps` one-shot dispatches, rotating over `copies`
+    binding sets; the first 3 dispatches are warmups (the reference's method,
+    tests/native/forward-vulkan.js:518-559: median of >= 10 after 3 warmups)."""
+    be.profile(True)
+    be.profile_select("dispatch:" + name)
+    ts = []
+    for i in range(reps + 3):
+        be.profile_reset()
+        be.dispatch(name, make_bindings(i % copies), push)
+        n, ms = be.profile_report()["dispatch:" + name]
+        if i >= 3:
+            ts.append(ms * 1000.0)
+    be.profile(False)
+    be.profile_select(None)
+    return float(np.median(ts)), float(np.min(ts))
+
+
+def kernel_times(be, name, make_bindings, push, copies, reps):
+    """Per-kernel median device times (us) of one named dispatch's launches."""
+    be.profile(True)
+    be.profile_select(None)
+    per = {}
+    for i in range(reps + 3):
+        be.profile_reset()
+        be.dispatch(name, make_bindings(i % copies), push)
+        if i >= 3:
+            for k, (n, ms) in be.profile_report().items():
+                if not k.startswith("dispatch:"):
+                    per.setdefault(k, []).append(ms * 1000.0)
+    be.profile(False)
+    return {k: round(float(np.median(v)), 3) for k, v in per.items()}
+
+
+def roof(achieved, peak, unit, traffic=None):
+    return {"bound": "hbm" if unit == "GB/s" else "mfma", "achieved": round(achieved, 2), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def bench_config(cfg_id, reps, variant="both", no_cpu=False, calib_mb=0):
+    """One JSON line for BASELINE config 1-4 (each kernel on its own, cache-warm
+    and cache-cold), with the roofline against MI355X peaks and the oracle CPU
+    baseline at both thread settings."""
+    import oracle
+    from textsift_amd import _native, synth
+    from textsift_amd.config import PF_CONFIG as cfg
+    be = _native.Backend(0)
+    if calib_mb:
+        run_calibration(be, calib_mb)
+    u32 = lambda *v: np.array(v, np.uint32).tobytes()
+    keep = []
+    nan2 = (float("nan"), float("nan"))
+    do_warm, do_cold = variant in ("both", "warm"), variant in ("both", "cold")
+
+    def buf(a=None, nbytes=None):
+        b = be.buffer(a) if a is not None else be.buffer(nbytes=nbytes)
+        keep.append(b)
+        return b
+
+    out = {"n_gpus": 1, "higher_is_better": False, "data": "synthetic (seeded)", "dtype": None}
+    if cfg_id == 1:
+        T, N, K = 512, 640, 640
+        x = synth.to_fp16_bits(synth.normal(1, T * K)).reshape(T, K)
+        w = synth.qweight(2, N, K, zp=8, bias_sigma=None)
+        alg_bytes = T * K * 2 + N * K // 2 + N * (K // 32) * 2 + T * N * 2
+        flops = 2.0 * T * N * K
+        ws = alg_bytes + N * (K // 32) * 4
+        copies = max(1, CACHE_COLD_BYTES // ws) if do_cold else 1
+        sets = []
+        for c in range(copies):
+            wq, ws_, wz = buf(w["int4"]), buf(w["scales"]), buf(w["zp"])
+            w4, sz = buf(nbytes=N * K // 2), buf(nbytes=N * (K // 32) * 4)
+            be.dispatch("w4_prepare", [wq, ws_, wz, w4, sz], u32(N, K, 1, 0))
+            for b_ in (wq, ws_, wz):
+                b_.release()
+            sets.append([buf(x), w4, sz, buf(w["bias"]), buf(nbytes=T * N * 2)])
+        push = u32(T, N, K, 0, 0, 0)
+        name = "matmul_w4"
+        warm = time_dispatch(be, name, lambda i: sets[0], push, 1, reps) if do_warm else nan2
+        cold = time_dispatch(be, name, lambda i: sets[i], push, copies, reps) if do_cold else nan2
+        got = sets[0][4].read(np.uint16).reshape(T, N)
+        ref = oracle.matmul(x, w["int4"], w["scales"], w["zp"], w["bias"], N, K, x_f32=False, out_f32=False)
+        err = float(np.linalg.norm(got.view(np.float16).astype(np.float64) - ref.view(np.float16))
+                    / np.linalg.norm(ref.view(np.float16).astype(np.float64)))
+
+        def cpu(nt):
+            sliced(lambda lo, hi: oracle.matmul(x[lo:hi], w["int4"], w["scales"], w["zp"], w["bias"], N, K, False,
+                                                False), T, nt)
+        reps_cpu = 20
+        cpu_b = None if no_cpu else cpu_baseline_both(lambda nt: [cpu(nt) for _ in range(reps_cpu)], reps_cpu * flops / 1e9, "GFLOP/s",
+                                  f"{reps_cpu} x the config's GEMM (oracle MatMulNBits, T-slices)")
+        out.update({"metric": "int4 GEMM 512x640x640 (fp16 in/out, blk32, zp 8) us/launch", "dtype": "int4w/fp16/f32-acc",
+                    "config": {"workload": "BASELINE config 1: MatMulNBits int4 GEMM T=512 N=640 K=640",
+                               "kernel": "k_gemm_w4 all-K 16-token tile (the forward's choice at 512 rows)"},
+                    "algorithmic": {"bytes": alg_bytes, "flops": flops},
+                    "value": round(warm[0] if do_warm else cold[0], 3), "unit": "us", "rel_err_vs_oracle": err})
+        for tag, (med, mn) in (("warm", warm), ("cold", cold)):
+            out[tag] = {"median_us": round(med, 3), "min_us": round(mn, 3),
+                        "hbm": roof(alg_bytes / (med * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"),
+                        "mfma": roof(flops / (med * 1e-6) / 1e12, MFMA_FP16_PEAK_TFLOPS, "TFLOP/s")}
+        out["cold"]["rotating_copies"] = copies
+        out["roofline"] = out["cold"]["hbm"]
+        out["roofline_time_us"] = round(max(alg_bytes / (HBM_PEAK_GBS * 1e3), flops / (MFMA_FP16_PEAK_TFLOPS * 1e6)), 3)
+        out["cpu_baseline"] = cpu_b
+        out["gpu_cpu_ratio"] = round(flops / (warm[0] * 1e-6) / 1e9 / cpu_b["value"], 1) if cpu_b else None
+    elif cfg_id == 2:
+        V, D, T = cfg.vocab_size, cfg.hidden_size, 32768
+        tab = synth.qweight(3, V, D, zp=8, bias_sigma=None)
+        ids = synth.token_ids(4, T, V)
+        rows = len(np.unique(ids))
+        alg_bytes = T * 4 + rows * (D // 2 + (D // 32) * 2 + (D // 64)) + T * D * 2
+        tab_bytes = tab["int4"].nbytes + tab["scales"].nbytes + tab["zp"].nbytes
+        copies = max(1, -(-CACHE_COLD_BYTES // (tab_bytes + T * D * 2))) if do_cold else 1
+        sets = [[buf(tab["int4"]), buf(tab["scales"]), buf(tab["zp"]), buf(ids), buf(nbytes=T * D * 2)]
+                for _ in range(copies)]
+        push = u32(T, V, D, 0)
+        name = "embed_lookup_int4"
+        warm = time_dispatch(be, name, lambda i: sets[0], push, 1, reps) if do_warm else nan2
+        cold = time_dispatch(be, name, lambda i: sets[i], push, copies, reps) if do_cold else nan2
+        got = sets[0][4].read(np.uint16).reshape(T, D)
+        ref = oracle.embed_lookup(tab["int4"], tab["scales"], tab["zp"], ids, V, D)
+        exact = bool(np.array_equal(got, ref))
+
+        def cpu(nt):
+            sliced(lambda lo, hi: oracle.embed_lookup(tab["int4"], tab["scales"], tab["zp"], ids[lo:hi], V, D), T, nt)
+        reps_cpu = 10
+        cpu_b = None if no_cpu else cpu_baseline_both(lambda nt: [cpu(nt) for _ in range(reps_cpu)], reps_cpu * alg_bytes / 1e9, "GB/s",
+                                  f"{reps_cpu} x the config's gather (oracle embed_lookup_int4, T-slices)")
+        out.update({"metric": "GatherBlockQuantized 32768 ids x 640 (int4 table 200064 rows) us/launch",
+                    "dtype": "u4->fp16", "config": {"workload": "BASELINE config 2: GatherBlockQuantized embedding",
+                                                    "kernel": "k_embed", "distinct_rows": rows},
+                    "algorithmic": {"bytes": alg_bytes}, "value": round(warm[0] if do_warm else cold[0], 3), "unit": "us",
+                    "bit_exact_vs_oracle": exact})
+        for tag, (med, mn) in (("warm", warm), ("cold", cold)):
+            out[tag] = {"median_us": round(med, 3), "min_us": round(mn, 3),
+                        "hbm": roof(alg_bytes / (med * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s")}
+        out["cold"]["rotating_copies"] = copies
+        out["roofline"] = out["cold"]["hbm"]
+        out["roofline_time_us"] = round(alg_bytes / (HBM_PEAK_GBS * 1e3), 3)
+        out["cpu_baseline"] = cpu_b
+        out["gpu_cpu_ratio"] = round(alg_bytes / (warm[0] * 1e-6) / 1e9 / cpu_b["value"], 1) if cpu_b else None
+    elif cfg_id == 3:
+        T, D, E, K, F = 2048, cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.intermediate_size
+        x = synth.to_fp16_bits(synth.normal(5, T * D)).reshape(T, D)
+        rw_, rb = synth.zipf_router(6, D, E)
+        gu = synth.qweight(7, 2 * F, D, lead=(E,))
+        dn = synth.qweight(8, D, F, lead=(E,))
+        exp_bytes = sum(gu[k].nbytes for k in ("int4", "scales", "zp", "bias")) + \
+            sum(dn[k].nbytes for k in ("int4", "scales", "zp", "bias"))
+        prep_bytes = E * 2 * F * (D // 2 + (D // 32) * 4 + 2) + E * D * (F // 2 + (F // 32) * 4 + 2)
+        copies = max(1, -(-CACHE_COLD_BYTES // prep_bytes)) if do_cold else 1
+        wsets = []
+        for c in range(copies):
+            pw = []
+            for qw, rows, kk in ((gu, 2 * F, D), (dn, D, F)):
+                wq, ws_, wz = buf(qw["int4"]), buf(qw["scales"]), buf(qw["zp"])
+                w4, sz = buf(nbytes=E * rows * kk // 2), buf(nbytes=E * rows * (kk // 32) * 4)
+                be.dispatch("w4_prepare", [wq, ws_, wz, w4, sz], u32(E * rows, kk, 1, 0))
+                for b_ in (wq, ws_, wz):
+                    b_.release()
+                pw += [w4, sz, buf(qw["bias"])]
+            wsets.append(pw)
+        xb, rwb, rbb = buf(x), buf(rw_), buf(rb)
+        ob, ib, wb = buf(nbytes=T * D * 2), buf(nbytes=T * K * 4), buf(nbytes=T * K * 4)
+        push = u32(T, D, E, K, F, 0, 0, 0)
+        name = "moe_ffn_w4"
+        mk = lambda i: [xb, rwb, rbb] + wsets[i] + [ob, ib, wb]
+        warm = time_dispatch(be, name, lambda i: mk(0), push, 1, reps) if do_warm else nan2
+        cold = time_dispatch(be, name, mk, push, copies, reps) if do_cold else nan2
+        per_kernel = kernel_times(be, name, lambda i: mk(0), push, 1, max(5, reps // 2))
+        ridx = ib.read(np.int32).reshape(T, K)
+        rwt = wb.read(np.float32).reshape(T, K)
+        y = ob.read(np.uint16).reshape(T, D)
+        counts = np.bincount(ridx.ravel(), minlength=E)
+        srt = np.sort(counts)[::-1]
+        nz = srt[srt > 0]
+        rank = np.arange(1, nz.size + 1)
+        zipf_s = float(-np.polyfit(np.log(rank), np.log(nz), 1)[0])
+        touched = int((counts > 0).sum())
+        alg_flops = 2.0 * T * D * E + 2.0 * T * K * (2 * F * D + D * F)
+        alg_bytes = int(touched / E * exp_bytes) + D * E * 2 + E * 2 + T * D * 2 * 2 + T * K * 8
+        w = {}
+        for kk, vv in gu.items():
+            w[f"layers.0.experts.gate_up.{kk}"] = vv
+        for kk, vv in dn.items():
+            w[f"layers.0.experts.down.{kk}"] = vv
+        for nm in ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.o_proj", "router"):
+            for kk, vv in synth.qweight(9, 64, 64).items():
+                w[f"layers.0.{nm}.{kk}"] = vv
+        w["layers.0.input_layernorm"] = w["layers.0.post_attention_layernorm"] = np.zeros(D, np.uint16)
+        w["layers.0.attn.sinks"] = np.zeros(cfg.num_heads, np.float32)
+        xf = oracle.fp16_to_f32(x)
+        ref = oracle.expert_dispatch(cfg, w, 0, xf, ridx, rwt * np.float32(0.25), n_slices=8)
+        err = float(np.linalg.norm(y.view(np.float16).astype(np.float64) - ref.view(np.float16))
+                    / np.linalg.norm(ref.view(np.float16).astype(np.float64)))
+        wr = oracle.fp16_to_f32(rw_).reshape(D, E)
+        br = oracle.fp16_to_f32(rb)
+
+        def cpu(nt):
+            lg = np.empty((T, E), np.float32)
+            sliced(lambda lo, hi: np.matmul(xf[lo:hi], wr, out=lg[lo:hi]), T, nt)
+            lg += br
+            ix, vals = oracle.topk(lg, T, E, K)
+            sm = oracle.softmax(vals, T, K)
+            oracle.expert_dispatch(cfg, w, 0, xf, ix, sm * np.float32(0.25), n_slices=nt)
+        cpu_b = None if no_cpu else cpu_baseline_both(cpu, alg_flops / 1e9, "GFLOP/s",
+                                  "the config's MoE layer: router (numpy f32), oracle top-k/softmax and expert-major "
+                                  "dispatch (token slices)")
+        out.update({"metric": "MoE FFN layer T=2048, 128 experts top-4, Zipf(1.1) router us/layer",
+                    "dtype": "int4w/fp16-mfma/f32-acc",
+                    "config": {"workload": "BASELINE config 3: one MoE FFN layer", "kernels": per_kernel,
+                               "expert_tile": 64},
+                    "algorithmic": {"flops": alg_flops, "bytes": alg_bytes, "experts_touched": touched},
+                    "zipf": {"fitted_s": round(zipf_s, 3), "max_load": int(srt[0]), "min_load": int(srt[-1]),
+                             "top8_share": round(float(srt[:8].sum() / srt.sum()), 4),
+                             "loads_sorted": [int(v) for v in srt]},
+                    "value": round(warm[0] if do_warm else cold[0], 3), "unit": "us", "rel_err_vs_oracle": err})
+        for tag, (med, mn) in (("warm", warm), ("cold", cold)):
+            out[tag] = {"median_us": round(med, 3), "min_us": round(mn, 3),
+                        "hbm": roof(alg_bytes / (med * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"),
+                        "mfma": roof(alg_flops / (med * 1e-6) / 1e12, MFMA_FP16_PEAK_TFLOPS, "TFLOP/s")}
+        out["cold"]["rotating_copies"] = copies
+        out["roofline"] = out["cold"]["hbm"]
+        out["roofline_time_us"] = round(max(alg_bytes / (HBM_PEAK_GBS * 1e3),
+                                            alg_flops / (MFMA_FP16_PEAK_TFLOPS * 1e6)), 3)
+        out["cpu_baseline"] = cpu_b
+        out["gpu_cpu_ratio"] = round(alg_flops / (warm[0] * 1e-6) / 1e9 / cpu_b["value"], 1) if cpu_b else None
+    elif cfg_id == 4:
+        T, Hq, Hkv, hd, W = 8192, 14, 2, 64, 128
+        q = synth.to_fp16_bits(synth.normal(10, T * Hq * hd)).reshape(T, Hq * hd)
+        k = synth.to_fp16_bits(synth.normal(11, T * Hkv * hd)).reshape(T, Hkv * hd)
+        v = synth.to_fp16_bits(synth.normal(12, T * Hkv * hd)).reshape(T, Hkv * hd)
+        sinks = np.full(Hq, -np.inf, np.float32)
+        alg_bytes = 2 * q.nbytes + k.nbytes + v.nbytes
+        t = np.arange(T)
+        keys = float((np.minimum(T, t + W + 1) - np.maximum(0, t - W)).sum())
+        flops = 4.0 * hd * Hq * keys
+        copies = max(1, -(-CACHE_COLD_BYTES // alg_bytes)) if do_cold else 1
+        sets = [[buf(q), buf(k), buf(v), buf(sinks), buf(np.ones(T, np.uint8)), buf(nbytes=q.nbytes)]
+                for _ in range(copies)]
+        push = u32(T, Hq, Hkv, hd, W, 0) + np.array([0.125], np.float32).tobytes() + u32(1)
+        name = "banded_attention"
+        warm = time_dispatch(be, name, lambda i: sets[0], push, 1, reps) if do_warm else nan2
+        cold = time_dispatch(be, name, lambda i: sets[i], push, copies, reps) if do_cold else nan2
+        got = sets[0][5].read(np.uint16).reshape(T, Hq * hd)
+        # scale 1/8 applied to Q in fp16 is exact (a power of two, no subnormal results for N(0,1) inputs)
+        qs = synth.to_fp16_bits(oracle.fp16_to_f32(q) * np.float32(0.125)).reshape(T, Hq * hd)
+        ref = oracle.banded_attention_wgsl(qs, k, v, sinks, None, T, Hq, Hkv, hd, W)
+        err = float(np.linalg.norm(got.view(np.float16).astype(np.float64) - ref.view(np.float16))
+                    / np.linalg.norm(ref.view(np.float16).astype(np.float64)))
+
+        def cpu(nt):
+            sliced(lambda h0, h1: oracle.banded_attention(qs, k, v, sinks, None, T, Hq, Hkv, hd, W, h0, h1), Hq, nt)
+        cpu_b = None if no_cpu else cpu_baseline_both(cpu, flops / 1e9, "GFLOP/s",
+                                  "the config's attention (oracle banded_attention, H_q slices, attention.ts:156-182)")
+        out.update({"metric": "banded GQA attention T=8192 14/2 heads d=64 +-128 us/launch", "dtype": "fp16/f32-acc",
+                    "config": {"workload": "BASELINE config 4: banded bidirectional GQA attention, scale 1/8, no sinks",
+                               "kernel": "k_banded_attention_hw"},
+                    "algorithmic": {"bytes": alg_bytes, "flops": flops}, "value": round(warm[0] if do_warm else cold[0], 3), "unit": "us",
+                    "rel_err_vs_oracle": err})
+        for tag, (med, mn) in (("warm", warm), ("cold", cold)):
+            out[tag] = {"median_us": round(med, 3), "min_us": round(mn, 3),
+                        "hbm": roof(alg_bytes / (med * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"),
+                        "mfma": roof(flops / (med * 1e-6) / 1e12, MFMA_FP16_PEAK_TFLOPS, "TFLOP/s")}
+        out["cold"]["rotating_copies"] = copies
+        out["roofline"] = out["cold"]["hbm"]
+        out["roofline_time_us"] = round(max(alg_bytes / (HBM_PEAK_GBS * 1e3), flops / (MFMA_FP16_PEAK_TFLOPS * 1e6)), 3)
+        out["cpu_baseline"] = cpu_b
+        out["gpu_cpu_ratio"] = round(flops / (warm[0] * 1e-6) / 1e9 / cpu_b["value"], 1) if cpu_b else None
+    else:
+        raise SystemExit(f"unknown config {cfg_id}")
+    for b_ in keep:
+        b_.release()
+    be.close()
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5],
+                    help="BASELINE config: 5 = the full forward (default); 1-4 = one kernel on its own")
+    ap.add_argument("--reps", type=int, default=20, help="timed dispatches per variant for --config 1-4")
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--seq", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=20260101)
-    ap.add_argument("--cpu-seqs", type=int, default=3,
+    ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="CPU baseline sample: this many of the batch's sequences (full length) through the oracle")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -327,6 +718,9 @@ def main():
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--copy-mb", type=int, default=1024)
+    ap.add_argument("--raw-symbols", action="store_true", help="--traffic-report: group by kernel symbol")
+    ap.add_argument("--variant", choices=["both", "warm", "cold"], default="both",
+                    help="--config 1-4: which cache variants to time (one alone for rocprofv3 runs)")
     ap.add_argument("--sq-report", nargs=2, metavar=("PASS1_CSV", "PASS2_CSV"),
                     help="summarise two rocprofv3 --pmc passes of the counters in SQ_PASS1 / SQ_PASS2")
     ap.add_argument("--blas-reference", action="store_true",
@@ -351,7 +745,7 @@ def main():
         blas_ref = json.loads(r.stdout.strip().splitlines()[-1])
 
     if args.traffic_report:
-        print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb))
+        print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb, raw=args.raw_symbols))
         return
     if args.sq_report:
         print(sq_report(args.sq_report[0], args.sq_report[1]))
@@ -361,6 +755,10 @@ def main():
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(across GPUs the forward shards as independent sequences, one process per GPU)", file=sys.stderr)
         sys.exit(2)
+
+    if args.config != 5:
+        bench_config(args.config, args.reps, args.variant, args.no_cpu, args.copy_calibration_mb)
+        return
 
     from textsift_amd import _native, synth
     from textsift_amd.config import PF_CONFIG
@@ -389,11 +787,7 @@ def main():
         model.forward_device(ids_buf, None, B, T, logits_buf)
 
     if args.copy_calibration_mb:
-        n = args.copy_calibration_mb << 20
-        src, dst = be.buffer(nbytes=n), be.buffer(nbytes=n)
-        be.dispatch("copy16", [src, dst], np.array([n], np.uint32))
-        src.release()
-        dst.release()
+        run_calibration(be, args.copy_calibration_mb)
 
     # per-kernel table: a separate profiled pass with every launch bracketed
     prof, dom = {}, None
@@ -449,17 +843,32 @@ def main():
 
     cpu = None
     if not args.no_cpu:
+        # the oracle (C restatement of the WASM path, the reference's MtPool
+        # partitioning) on whole sequences of the batch: all host cores (<= 16,
+        # the box's CPU share) and the reference's default worker count; the
+        # sequences run one after another as the reference runs its chunks, so
+        # tokens/s of the sample is that of the whole 16-sequence batch
         import oracle
+        n_host, model = host_cpu()
         thr = args.cpu_threads or cpu_threads()
+        refc = ref_default_threads(n_host)
+
+        def cpu_rate(nthr, nseq):
+            t2 = time.perf_counter()
+            for b in range(nseq):
+                oracle.model_forward(cfg, weights, ids[b * T:(b + 1) * T], n_threads=nthr)
+            return nseq * T / (time.perf_counter() - t2), time.perf_counter() - t2
+
         nseq = max(1, min(args.cpu_seqs, B))
-        t2 = time.perf_counter()
-        for b in range(nseq):
-            oracle.model_forward(cfg, weights, ids[b * T:(b + 1) * T], n_threads=thr)
-        t3 = time.perf_counter()
-        cpu = {"value": round(nseq * T / (t3 - t2), 2), "unit": "tokens/s", "cores": thr, "kind": "port",
-               "sample": f"the first {nseq} of the batch's {B} sequences ({nseq}x{T} tokens, same model and ids) "
-                         f"through the oracle (C restatement of the WASM path, MtPool partitioning on {thr} "
-                         f"threads), {t3 - t2:.1f} s"}
+        v_all, s_all = cpu_rate(thr, nseq)
+        v_ref, s_ref = cpu_rate(refc, 1) if refc != thr else (v_all, 0.0)
+        cpu = {"value": round(v_all, 2), "unit": "tokens/s", "cores": thr, "kind": "port",
+               "sample": f"{nseq} of the batch's {B} sequences ({nseq}x{T} tokens, same model and ids, {s_all:.1f} s) "
+                         f"through the oracle (C restatement of the WASM path, MtPool partitioning on {thr} threads); "
+                         f"the batch's sequences run serially, so this rate extrapolates to all {B}",
+               "host_nproc": n_host, "cpu_model": model,
+               "reference_default_threads": {"cores": refc, "value": round(v_ref, 2),
+                                             "sample": f"1 sequence ({T} tokens, {s_ref:.1f} s)"}}
 
     be.close()
     out = {
@@ -474,6 +883,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4w/fp16-mfma/f32-acc",
+        "precision": "fp16 (PFHIP_PRECISION_FP16: fp16 GEMM inputs, block scale folded into fp16 weights)",
         "data": "synthetic (seeded random-init int4 weights, uniform token ids)",
         "config": {"workload": "full synthetic 8-layer int4 MoE encoder forward (BASELINE config 5)",
                    "batch": B, "seq_len": T, "layers": cfg.num_layers, "experts": cfg.num_experts,

@@ -863,7 +863,53 @@ __global__ void k_copy16(const u4_t* __restrict__ src, u4_t* __restrict__ dst, s
     dst[i] = src[i];
 }
 
+// The same copy with the loads going HBM -> LDS directly
+// (global_load_lds_dwordx4, as the GEMMs load their activations), then LDS ->
+// registers -> HBM: the counters' factor for that load form.
+__global__ __launch_bounds__(256) void k_copy16_lds(const u4_t* __restrict__ src, u4_t* __restrict__ dst, size_t n) {
+  __shared__ __attribute__((aligned(16))) u4_t stage[256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (size_t base = (size_t)blockIdx.x * 256; base < n; base += (size_t)gridDim.x * 256) {
+    const size_t i = min(base + threadIdx.x, n - 1);  // lanes past n re-read the last unit (not stored)
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(src + i, (__attribute__((address_space(3))) void*)(stage + wave * 64), 16, 0, 0);
+#endif
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (base + threadIdx.x < n) dst[base + threadIdx.x] = stage[wave * 64 + lane];
+    __syncthreads();
+  }
+}
+
+// dst[i] = table[idx[i]] in 16-byte units: scattered 16-byte reads, as the
+// embedding gather and the expert GEMMs' row gathers make them.
+__global__ void k_gather16(const u4_t* __restrict__ table, const int32_t* __restrict__ idx, u4_t* __restrict__ dst,
+                           size_t n, uint32_t table_units) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = table[(uint32_t)idx[i] % table_units];
+}
+
 }  // namespace
+
+void copy16_lds(pfhip_backend* b, const void* src, void* dst, size_t bytes) {
+  PF_CHECK(bytes % 16 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0,
+           "copy16_lds: 16-byte aligned sizes and pointers");
+  if (!bytes) return;
+  ProfScope ps(b, "copy16_lds");
+  hipLaunchKernelGGL(k_copy16_lds, dim3(4096), dim3(256), 0, b->stream, static_cast<const u4_t*>(src),
+                     static_cast<u4_t*>(dst), bytes / 16);
+  PF_HIP(hipGetLastError());
+}
+
+void gather16(pfhip_backend* b, const void* table, uint32_t table_units, const int32_t* idx, void* dst, size_t n) {
+  PF_CHECK(table_units > 0 && ((uintptr_t)table & 15) == 0 && ((uintptr_t)dst & 15) == 0,
+           "gather16: 16-byte aligned table and output, non-empty table");
+  if (!n) return;
+  ProfScope ps(b, "gather16");
+  hipLaunchKernelGGL(k_gather16, dim3(4096), dim3(256), 0, b->stream, static_cast<const u4_t*>(table), idx,
+                     static_cast<u4_t*>(dst), n, table_units);
+  PF_HIP(hipGetLastError());
+}
 
 void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes) {
   PF_CHECK(bytes % 16 == 0 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0,

@@ -247,8 +247,12 @@ void qmoe_down_scatter_ref(pfhip_backend* b, const float* glu, const int32_t* ri
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)PFHIP_NOALLOC_SCRATCH_MIB << 20;
 void* noalloc_scratch(int device);
 
-// Plain device copy of `bytes` (multiple of 16, 16-byte aligned).
+// Plain device copy of `bytes` (multiple of 16, 16-byte aligned), and the
+// calibration workloads of known size for the HBM counters: the same copy
+// with HBM -> LDS loads, and a gather of n 16-byte units at idx[i] % table_units.
 void copy16(pfhip_backend* b, const void* src, void* dst, size_t bytes);
+void copy16_lds(pfhip_backend* b, const void* src, void* dst, size_t bytes);
+void gather16(pfhip_backend* b, const void* table, uint32_t table_units, const int32_t* idx, void* dst, size_t n);
 
 // Exhaustive checks of the fast math helpers (tests only): which = 0 checks
 // div_one_plus against IEEE division, 1 checks exp_approx_fast against

@@ -99,6 +99,8 @@ struct KernelEntry {
   uint32_t n_bindings;
   size_t push_bytes;
   std::function<void(pfhip_backend*, pfhip_buffer* const*, const uint8_t*)> run;
+  // profiling name of the whole dispatch ("dispatch:<name>"), all its launches together
+  std::string prof_name = std::string("dispatch:") + name;
 };
 
 template <class T>
@@ -153,6 +155,59 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
   a.N = N;
   a.K = K;
   gemm_int4(b, a, x_f32 ? XKind::SPLIT : XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, T >= 2048 ? 128 : 64, name);
+}
+
+// The MoE FFN layer of BASELINE config 3 in the forward's fp16 numerics, on
+// weights already in the gemm_w4 form (w4_prepare): fp16 router W [D][E]
+// (+ bias) -> router_topk -> routing plan -> gate_up grouped GEMM + SwiGLU
+// (fp16 out) -> down grouped GEMM (f32 out) -> combine into fp16 out.
+// Expert tiles as the forward chooses them (expert_tile).
+static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw, const uint16_t* rb,
+                         const uint32_t* guw, const uint32_t* gus, const uint16_t* gub, const uint32_t* dnw,
+                         const uint32_t* dns, const uint16_t* dnb, uint16_t* out, int32_t* ridx, float* rwt, int T,
+                         int D, int E, int K, int F) {
+  const ExpertTile et = expert_tile(T, K, E, true, D, F);
+  const size_t S = (size_t)T * K;
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t plan_b = moe_plan_bytes(T, K, E, et.t);
+  const size_t bytes = al((size_t)T * E * 4) + al(S * F * 2) + al(S * D * 4) + al((size_t)T * D * 2) + plan_b;
+  char* s = static_cast<char*>(backend_scratch(b, bytes));
+  float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
+  uint16_t* glu = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
+  float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
+  uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
+  MoePlan m = moe_plan_carve(s, T, K, E, et.t);
+  router_f16w(b, x, rw, rb, logits, T, D, E);
+  router_topk(b, logits, ridx, rwt, T, E, K, 1.0f);
+  moe_route(b, ridx, T, K, E, m);
+  GemmArgs g;
+  g.x = x; g.ldx = D; g.row_map = m.slot_token;
+  g.w = reinterpret_cast<const uint8_t*>(guw); g.wsz = gus; g.wsz_gs = (size_t)2 * F * (D / 32);
+  g.w_gs = (size_t)2 * F * D / 2; g.bias = gub; g.bias_gs = (size_t)2 * F;
+  g.out = glu; g.ldo = F; g.M = (int)S; g.N = 2 * F; g.K = D;
+  g.tiles = m.tiles; g.num_tiles = m.num_tiles; g.max_tiles = m.max_tiles;
+  gemm_w4(b, g, XKind::F16, Epi::SWIGLU_F16, true, et.t, et.wf, "moe_gate_up");
+  GemmArgs d;
+  d.x = glu; d.ldx = F;
+  d.w = reinterpret_cast<const uint8_t*>(dnw); d.wsz = dns; d.wsz_gs = (size_t)D * (F / 32);
+  d.w_gs = (size_t)D * F / 2; d.bias = dnb; d.bias_gs = (size_t)D;
+  d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
+  d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
+  gemm_w4(b, d, XKind::F16, Epi::F32, true, et.t, et.wf, "moe_down");
+  // out = fp16(sum_k w_k y_k) (zero residual -> the output holds the MoE output)
+  zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
+  moe_combine(b, ridx, rwt, m.slot_of, y, zero_res, nullptr, out, T, K, D);
+}
+
+// Dense GEMM of the fp16 forward on prepared weights, tile as the forward
+// chooses it for T rows when tile_t == 0.
+static void matmul_w4_auto(pfhip_backend* b, GemmArgs& a, Epi epi, int tile_t, int wf, const char* name) {
+  if (tile_t == 0) {
+    const bool sm = a.M <= 2048 && (a.K == 640 || a.K == 896);
+    tile_t = sm ? 16 : 128;
+    wf = sm ? 1 : 4;
+  }
+  gemm_w4(b, a, XKind::F16, epi, false, tile_t, wf, "matmul_w4");
 }
 
 static std::vector<KernelEntry>& registry() {
@@ -300,6 +355,22 @@ static std::vector<KernelEntry>& registry() {
                  need(bs, 1, n, "copy16");
                  copy16(b, bs[0]->ptr, bs[1]->ptr, n);
                }});
+  // copy16_lds: bindings [src, dst], push {bytes}; the copy with HBM -> LDS loads
+  r.push_back({"copy16_lds", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const size_t n = pu(p, 0);
+                 need(bs, 0, n, "copy16_lds");
+                 need(bs, 1, n, "copy16_lds");
+                 copy16_lds(b, bs[0]->ptr, bs[1]->ptr, n);
+               }});
+  // gather16: bindings [table, idx i32 [n], dst [n][16 B]], push {n, table_units}
+  r.push_back({"gather16", 3, 8, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const size_t n = pu(p, 0);
+                 const uint32_t tu = pu(p, 1);
+                 need(bs, 0, (size_t)tu * 16, "gather16");
+                 need(bs, 1, n * 4, "gather16");
+                 need(bs, 2, n * 16, "gather16");
+                 gather16(b, bs[0]->ptr, tu, bp<int32_t>(bs, 1), bs[2]->ptr, n);
+               }});
   // probe_fast_math: push {which, lo, hi}; binding [out u32 x3]
   r.push_back({"probe_fast_math", 1, 12, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  need(bs, 0, 12, "probe_fast_math");
@@ -375,6 +446,66 @@ static std::vector<KernelEntry>& registry() {
                  a.topk_k = 4;
                  a.topk_wscale = 1.0f;
                  gemm_w4(b, a, XKind::F16, Epi::F32_TOPK, false, tile_t, 2, "matmul_int4_w4_topk");
+               }});
+  // w4_prepare: a MatMulNBits weight [rows][K] (+ scales, zero-points) into the gemm_w4 form.
+  // push {rows, K, has_zp, 0}; bindings [w_int4, scales, zp (ignored if has_zp == 0), w4 out [rows][K/8] u32,
+  // sz out [rows][K/32] u32]
+  r.push_back({"w4_prepare", 5, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int rows = (int)pu(p, 0), K = (int)pu(p, 1);
+                 const bool zp = pu(p, 2) != 0;
+                 PF_CHECK(rows > 0 && K > 0 && K % 32 == 0, "w4_prepare: bad shape");
+                 const int nb = K / 32;
+                 need(bs, 0, (size_t)rows * K / 2, "w4_prepare");
+                 need(bs, 1, (size_t)rows * nb * 2, "w4_prepare");
+                 if (zp) need(bs, 2, (size_t)rows * ((nb + 1) / 2), "w4_prepare");
+                 need(bs, 3, (size_t)rows * K / 2, "w4_prepare");
+                 need(bs, 4, (size_t)rows * nb * 4, "w4_prepare");
+                 w4_prepare(b, bp<uint8_t>(bs, 0), bp<uint16_t>(bs, 1), zp ? bp<uint8_t>(bs, 2) : nullptr,
+                            bp<uint32_t>(bs, 3), bp<uint32_t>(bs, 4), rows, K);
+               }});
+  // matmul_w4: the fp16 forward's GEMM on prepared weights (w4_prepare output).
+  // push {T, N, K, out_f32, tile_t (0: the forward's choice for T rows), wf};
+  // bindings [x fp16 [T][K], w4, sz, bias fp16 [N], out [T][N]]
+  r.push_back({"matmul_w4", 5, 24, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), N = (int)pu(p, 1), K = (int)pu(p, 2);
+                 const bool out_f32 = pu(p, 3) != 0;
+                 PF_CHECK(K % 128 == 0, "matmul_w4: K must be a multiple of 128");
+                 need(bs, 0, (size_t)T * K * 2, "matmul_w4");
+                 need(bs, 1, (size_t)N * K / 2, "matmul_w4");
+                 need(bs, 2, (size_t)N * (K / 32) * 4, "matmul_w4");
+                 need(bs, 3, (size_t)N * 2, "matmul_w4");
+                 need(bs, 4, (size_t)T * N * (out_f32 ? 4 : 2), "matmul_w4");
+                 GemmArgs a;
+                 a.x = bs[0]->ptr; a.ldx = K;
+                 a.w = bp<uint8_t>(bs, 1); a.wsz = bp<uint32_t>(bs, 2); a.bias = bp<uint16_t>(bs, 3);
+                 a.out = bs[4]->ptr; a.ldo = N; a.M = T; a.N = N; a.K = K;
+                 matmul_w4_auto(b, a, out_f32 ? Epi::F32 : Epi::F16, (int)pu(p, 4), (int)pu(p, 5), "matmul_w4");
+               }});
+  // moe_ffn_w4: moe_ffn in the fp16 numerics on prepared expert weights (BASELINE config 3 as the
+  // forward runs it). push {T, D, E, K, dff, 0, 0, 0}; bindings [x fp16 [T][D], router_w fp16 [D][E],
+  // router_bias fp16 [E], gu.w4, gu.sz, gu.bias, dn.w4, dn.sz, dn.bias, out fp16 [T][D], routing_idx [T][K],
+  // routing_w [T][K]]
+  r.push_back({"moe_ffn_w4", 12, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), D = (int)pu(p, 1), E = (int)pu(p, 2), K = (int)pu(p, 3);
+                 const int F = (int)pu(p, 4);
+                 PF_CHECK(T >= 1 && E >= K && K >= 1 && K <= 8, "moe_ffn_w4: bad T / E / K");
+                 PF_CHECK(D % 128 == 0 && F % 128 == 0, "moe_ffn_w4: D and dff must be multiples of 128");
+                 need(bs, 0, (size_t)T * D * 2, "moe_ffn_w4");
+                 need(bs, 1, (size_t)D * E * 2, "moe_ffn_w4");
+                 need(bs, 2, (size_t)E * 2, "moe_ffn_w4");
+                 need(bs, 3, (size_t)E * 2 * F * D / 2, "moe_ffn_w4");
+                 need(bs, 4, (size_t)E * 2 * F * (D / 32) * 4, "moe_ffn_w4");
+                 need(bs, 5, (size_t)E * 2 * F * 2, "moe_ffn_w4");
+                 need(bs, 6, (size_t)E * D * F / 2, "moe_ffn_w4");
+                 need(bs, 7, (size_t)E * D * (F / 32) * 4, "moe_ffn_w4");
+                 need(bs, 8, (size_t)E * D * 2, "moe_ffn_w4");
+                 need(bs, 9, (size_t)T * D * 2, "moe_ffn_w4");
+                 need(bs, 10, (size_t)T * K * 4, "moe_ffn_w4");
+                 need(bs, 11, (size_t)T * K * 4, "moe_ffn_w4");
+                 moe_ffn_fp16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), bp<uint32_t>(bs, 3),
+                              bp<uint32_t>(bs, 4), bp<uint16_t>(bs, 5), bp<uint32_t>(bs, 6), bp<uint32_t>(bs, 7),
+                              bp<uint16_t>(bs, 8), bp<uint16_t>(bs, 9), bp<int32_t>(bs, 10), bp<float>(bs, 11), T, D, E,
+                              K, F);
                }});
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -533,6 +664,7 @@ static void run_named(pfhip_backend* b, const char* name, pfhip_buffer* const* b
   }
   uint8_t pbuf[64] = {0};
   if (push_len) memcpy(pbuf, push, push_len);
+  ProfScope ps(b, k.prof_name.c_str());
   k.run(b, bindings, pbuf);
 }
 
