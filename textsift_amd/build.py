@@ -58,7 +58,33 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_addon(verbose)
     return LIB
+
+
+NODE_INCLUDE = os.environ.get("NODE_INCLUDE", "/usr/include/node")
+ADDON = os.path.join(LIBDIR, "textsift-hip.node")
+
+
+def build_addon(verbose: bool = True) -> str | None:
+    """The Node-API module (csrc/hip_napi.cc -> lib/textsift-hip.node), linked
+    against libpfhip.so next to it. Host code only: built with g++ against the
+    Node headers; skipped (None) when they are not installed."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        if verbose:
+            print(f"N-API module skipped: {NODE_INCLUDE}/node_api.h not found")
+        return None
+    tmp = ADDON + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-DNODE_GYP_MODULE_NAME=textsift_hip",
+           "-I" + NODE_INCLUDE, "-I" + os.path.join(ROOT, "include"), os.path.join(CSRC, "hip_napi.cc"),
+           "-L" + LIBDIR, "-lpfhip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"N-API module build failed:\n{r.stderr[-4000:]}")
+    os.replace(tmp, ADDON)
+    if verbose:
+        print(f"built {ADDON}")
+    return ADDON
 
 
 def clean():
