@@ -378,10 +378,16 @@ def test_attention_vs_oracle(be, T, W, masked, sinks, hw_exp):
     out = run(be, "banded_attention", [q, k, v, snk, mask], T * Hq * hd * 2,
               push(T, Hq, Hkv, hd, W, int(masked), sc, hw_exp)).view(np.uint16).reshape(T, Hq * hd)
     err, same = rel_err_norm(f16(out), f16(ref)), np.mean(out == ref)
+    ulps = fp16_ulp_diff(out, ref)
     print(f"attention T={T} W={W} masked={masked} sinks={sinks} hw_exp={hw_exp}: rel-err {err:.3e}, "
-          f"identical {same:.4f}")
+          f"identical {same:.4f}, max {ulps.max():.0f} fp16 ulp")
     assert err < 2e-3
-    assert same > 0.97
+    if hw_exp:
+        # the softmax weights enter P.V as fp16 (one rounding the shader does
+        # not make): ~1e-4 relative on the outputs
+        assert err < 5e-4 and same > 0.5
+    else:
+        assert same > 0.97
 
 
 # ---------------------------------------------------------------- routing

@@ -10,7 +10,9 @@ import os
 
 import numpy as np
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libpfhip.so")
+# PFHIP_LIBRARY names another build of the library (e.g. an installed copy)
+LIB_PATH = os.environ.get("PFHIP_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
+                                                           "libpfhip.so")
 ERR_CAP = 1024
 
 _lib = None

@@ -276,7 +276,7 @@ size_t scratch_layout(const pfhip_model_config& c, int M, Scr* s, void* base) {
   t.rw = (float*)take(S * 4);
   t.glu_hi = (uint16_t*)take(S * F * 2);
   t.glu_lo = (uint16_t*)take(S * F * 2);
-  t.y = (float*)take(S * D * 4);
+  t.y = (float*)take(S * D * (c.precision == PFHIP_PRECISION_FP16 ? 2 : 4));  // fp16 in the fp16 numerics
   t.logits16 = (uint16_t*)take((size_t)M * C * 2);
   t.logits = (float*)take((size_t)M * C * 4);
   t.plan = take(moe_plan_bytes(M, (int)K, (int)E, tt));
@@ -500,14 +500,15 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       if (f16) {
         d.w = reinterpret_cast<const uint8_t*>(L.down4.w); d.wsz = L.down4.sz;
         d.wsz_gs = (size_t)D * (F / 32);
-        gemm_w4(b, d, XKind::F16, Epi::F32, true, gw_t, gw_f, "gemm_moe_down");
+        // fp16 expert outputs (one rounding each; the combine widens them)
+        gemm_w4(b, d, XKind::F16, Epi::F16, true, gw_t, gw_f, "gemm_moe_down");
       } else {
         gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "gemm_moe_down");
       }
     }
     const uint16_t* gamma_next = l + 1 < m->layers.size() ? m->layers[l + 1].ln_in : W<uint16_t>(m, "final_norm");
-    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, s.h2, hn, gamma_next, s.xn_hi, f16 ? nullptr : s.xn_lo, M,
-                     K, D, c.eps);
+    moe_combine_norm(b, s.ridx, s.rw, plan.slot_of, s.y, f16, s.h2, hn, gamma_next, s.xn_hi, f16 ? nullptr : s.xn_lo,
+                     M, K, D, c.eps);
     record_tap(m, "h." + tag, hn, (size_t)M * D * 2);
     std::swap(h, hn);
   }

@@ -608,9 +608,11 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
 // NMODE: -1 = no norm; OUT_F16 / OUT_SPLIT = form of the next block's norm output.
 // NJ 256-element slices per row (3 covers D <= 768 with fewer registers
 // than the general 4, so more waves stay resident).
-template <int NMODE, int K, int NJ = MAXJ>
+// Y16: the expert outputs are fp16 (the fp16 numerics' down GEMM rounds them
+// once; widened here by the hardware), else f32.
+template <int NMODE, int K, int NJ = MAXJ, bool Y16 = false>
 __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__ idx, const float* __restrict__ w,
-                                                     const int32_t* __restrict__ slot_of, const float* __restrict__ y,
+                                                     const int32_t* __restrict__ slot_of, const void* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
                                                      uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
                                                      const uint16_t* __restrict__ gamma,
@@ -651,7 +653,15 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
     const int d = 4 * lane + 256 * j;
     if (d < D) {
 #pragma unroll
-      for (int k = 0; k < K; ++k) yv[j][k] = *reinterpret_cast<const f4_t*>(y + (size_t)sk[k] * D + d);
+      for (int k = 0; k < K; ++k) {
+        if constexpr (Y16) {
+          const h4_t h = __builtin_bit_cast(
+              h4_t, *reinterpret_cast<const u2_t*>(static_cast<const uint16_t*>(y) + (size_t)sk[k] * D + d));
+          yv[j][k] = f4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        } else {
+          yv[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)sk[k] * D + d);
+        }
+      }
       rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
       if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
     }
@@ -703,10 +713,17 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
 }
 
 template <int NMODE>
-void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
-                    const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
+void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
+                    bool y16, const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
                     uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
   const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+  if (y16) {  // the fp16 numerics (the model's K = 4, or any K up to 8 on 4 slices)
+    PF_CHECK(K == 4 && D <= 768, "moe_combine: fp16 expert outputs are built for K = 4, D <= 768");
+    hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3, true>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y,
+                       residual, moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);
+    PF_HIP(hipGetLastError());
+    return;
+  }
   if (D <= 768 && K == 4) {  // the model's shape
     hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
                        moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);
@@ -1151,24 +1168,26 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
   }
 }
 
-void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
-                 const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D) {
+void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
+                 bool y16, const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D) {
   PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K >= 1 && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine");
-  launch_combine<-1>(b, idx, w, slot_of, y, residual, moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
+  launch_combine<-1>(b, idx, w, slot_of, y, y16, residual, moe_out, h_out, nullptr, nullptr, nullptr, T, K, D, 0.0f);
 }
 
-void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const float* y,
-                      const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
+void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
+                      bool y16, const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps) {
   PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ && K >= 1 && K <= MAXK, "moe_combine: shape out of range");
   if (T <= 0) return;
   ProfScope ps(b, "moe_combine_norm");
   if (norm_lo)
-    launch_combine<OUT_SPLIT>(b, idx, w, slot_of, y, residual, nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D, eps);
+    launch_combine<OUT_SPLIT>(b, idx, w, slot_of, y, y16, residual, nullptr, h_out, gamma, norm_hi, norm_lo, T, K, D,
+                              eps);
   else
-    launch_combine<OUT_F16>(b, idx, w, slot_of, y, residual, nullptr, h_out, gamma, norm_hi, nullptr, T, K, D, eps);
+    launch_combine<OUT_F16>(b, idx, w, slot_of, y, y16, residual, nullptr, h_out, gamma, norm_hi, nullptr, T, K, D,
+                            eps);
 }
 
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,

@@ -165,8 +165,8 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
 static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw, const uint16_t* rb,
                          const uint32_t* guw, const uint32_t* gus, const uint16_t* gub, const uint32_t* dnw,
                          const uint32_t* dns, const uint16_t* dnb, uint16_t* out, int32_t* ridx, float* rwt, int T,
-                         int D, int E, int K, int F) {
-  const ExpertTile et = expert_tile(T, K, E, true, D, F);
+                         int D, int E, int K, int F, ExpertTile et) {
+  if (et.t == 0) et = expert_tile(T, K, E, true, D, F);
   const size_t S = (size_t)T * K;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t plan_b = moe_plan_bytes(T, K, E, et.t);
@@ -193,10 +193,10 @@ static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw
   d.w_gs = (size_t)D * F / 2; d.bias = dnb; d.bias_gs = (size_t)D;
   d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
   d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
-  gemm_w4(b, d, XKind::F16, Epi::F32, true, et.t, et.wf, "moe_down");
+  gemm_w4(b, d, XKind::F16, Epi::F16, true, et.t, et.wf, "moe_down");  // fp16 expert outputs, as the forward
   // out = fp16(sum_k w_k y_k) (zero residual -> the output holds the MoE output)
   zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
-  moe_combine(b, ridx, rwt, m.slot_of, y, zero_res, nullptr, out, T, K, D);
+  moe_combine(b, ridx, rwt, m.slot_of, y, true, zero_res, nullptr, out, T, K, D);
 }
 
 // Dense GEMM of the fp16 forward on prepared weights, tile as the forward
@@ -482,7 +482,8 @@ static std::vector<KernelEntry>& registry() {
                  matmul_w4_auto(b, a, out_f32 ? Epi::F32 : Epi::F16, (int)pu(p, 4), (int)pu(p, 5), "matmul_w4");
                }});
   // moe_ffn_w4: moe_ffn in the fp16 numerics on prepared expert weights (BASELINE config 3 as the
-  // forward runs it). push {T, D, E, K, dff, 0, 0, 0}; bindings [x fp16 [T][D], router_w fp16 [D][E],
+  // forward runs it). push {T, D, E, K, dff, tile_t, wf, 0} (tile_t 0: the forward's expert tile;
+  // else one of gemm_w4's tiles: (256, 4), (128, 4), (64, 5), (16, 1)); bindings [x fp16 [T][D], router_w fp16 [D][E],
   // router_bias fp16 [E], gu.w4, gu.sz, gu.bias, dn.w4, dn.sz, dn.bias, out fp16 [T][D], routing_idx [T][K],
   // routing_w [T][K]]
   r.push_back({"moe_ffn_w4", 12, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -505,7 +506,7 @@ static std::vector<KernelEntry>& registry() {
                  moe_ffn_fp16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), bp<uint32_t>(bs, 3),
                               bp<uint32_t>(bs, 4), bp<uint16_t>(bs, 5), bp<uint32_t>(bs, 6), bp<uint32_t>(bs, 7),
                               bp<uint16_t>(bs, 8), bp<uint16_t>(bs, 9), bp<int32_t>(bs, 10), bp<float>(bs, 11), T, D, E,
-                              K, F);
+                              K, F, ExpertTile{(int)pu(p, 5), (int)pu(p, 6)});
                }});
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -626,14 +627,14 @@ static std::vector<KernelEntry>& registry() {
                    gemm_w4(b, g, XKind::F16, Epi::SWIGLU_F16, true, et.t, et.wf, "moe_gate_up");
                    d.x_lo = nullptr;
                    d.w = reinterpret_cast<const uint8_t*>(dnw); d.wsz = dns; d.wsz_gs = (size_t)D * (F / 32);
-                   gemm_w4(b, d, XKind::F16, Epi::F32, true, et.t, et.wf, "moe_down");
+                   gemm_w4(b, d, XKind::F16, Epi::F16, true, et.t, et.wf, "moe_down");  // fp16 y, as the forward
                  } else {
                    gemm_int4(b, g, xk, Epi::SWIGLU_SPLIT, true, tt, "moe_gate_up");
                    gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "moe_down");
                  }
                  // out = fp16(sum_k w_k y_k) (zero residual -> h_out holds the MoE output)
                  zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
-                 moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, zero_res, nullptr,
+                 moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, f16, zero_res, nullptr,
                              bp<uint16_t>(bs, 13), T, K, D);
                }});
   r.push_back({"probe_mfma_f16", 3, 0, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*) {
