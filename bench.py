@@ -43,6 +43,7 @@ HBM_PEAK_GBS = 8000.0
 # rocprofv3 kernel symbols -> the launch names the backend profiles under
 KERNEL_LABELS = [
     ("gemm_moe_gate_up", ("k_gemm_w4<", "(pf::Epi)4, true")),
+    ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)0, true")),   # fp16 numerics: fp16 expert outputs
     ("gemm_moe_down", ("k_gemm_w4<", "(pf::Epi)1, true")),
     ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false")),
     ("gemm_o_add_rmsnorm", ("k_gemm_w4_rownorm",)),
