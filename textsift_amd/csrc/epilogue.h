@@ -66,6 +66,25 @@ __device__ __forceinline__ u2_t to_f16x4(const float v[4]) {
   return u2_t{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
 
+// to_f16x4 for data where exact zeros are common (the embedding's q == zp
+// values): zeros convert to zero on both paths, so only the nonzero
+// magnitudes are tested (and NaNs explicitly, which fminf / fmaxf skip).
+__device__ __forceinline__ u2_t to_f16x4_z(const float v[4]) {
+  float lo = 1.0f, hi = 0.0f;
+  bool nan = false;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float a = fabsf(v[r]);
+    lo = fminf(lo, a == 0.0f ? 1.0f : a);
+    hi = fmaxf(hi, a);
+    nan = nan | (v[r] != v[r]);
+  }
+  if (nan || !(lo >= 6.103515625e-05f && hi <= 65504.0f)) return to_f16x4_exact(f4_t{v[0], v[1], v[2], v[3]});
+  const h2_t a = __builtin_convertvector(f2_t{f32_fence(v[0]), f32_fence(v[1])}, h2_t);
+  const h2_t b = __builtin_convertvector(f2_t{f32_fence(v[2]), f32_fence(v[3])}, h2_t);
+  return u2_t{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+}
+
 // fp16 output of v with the RoPE rotation of pairs (n, n+1), (n+2, n+3)
 // (cs, sn: the two pairs' table entries at the row's sequence position).
 // The fast path needs every value that gets rounded to fp16 to lie in

@@ -15,41 +15,60 @@ namespace {
 constexpr int ROWS_PER_BLOCK = 4;  // one wave per row, 4 waves per block
 
 // ----------------------------------------------------------------------------
-// GatherBlockQuantized (embed_lookup_int4, :1523-1573): one thread per 8
-// values of an output row (one dword of packed nibbles, 16 output bytes).
-// fp16((q - zp) * scale) is a single rounding of an exact product, so the
-// output is bit-identical to the reference. Ids outside [0, V) give a zero row.
+// GatherBlockQuantized (embed_lookup_int4, :1523-1573). A thread takes one
+// dword of packed nibbles (8 output values, 16 bytes out) at the same
+// position u of EMB_TOK rows: it issues every id load, then every table
+// load, then converts and stores, so a wave has that many independent
+// memory chains in flight and the grid is a few rounds of waves. Consecutive
+// threads take consecutive dwords of a row: every wave's stores of one row
+// form a contiguous block, and the 4 threads of a quant block read its scale
+// and zero-point from one line. fp16((q - zp) * scale) is a single rounding of
+// an exact product, so the output is bit-identical to the reference. Ids
+// outside [0, V) give a zero row.
+constexpr int EMB_TOK = 4;  // measured: 2, 4 and 8 within 5 %, 16 slower
 __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
                                                const uint8_t* __restrict__ zp, const int32_t* __restrict__ ids,
                                                uint16_t* __restrict__ out, int T, int V, int D) {
-  // one thread per quant block: 16 bytes of nibbles, its scale and zero-point
-  // -> 32 fp16 values (64 contiguous output bytes); consecutive threads take
-  // consecutive blocks of a row, so loads and stores are contiguous per row
-  const int nb = D >> 5;
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)T * nb) return;
-  const int t = (int)(i / nb), blk = (int)(i % nb);
-  const int id = ids[t];
-  u4_t res[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-  if (id >= 0 && id < V) {
-    const size_t row = (size_t)id;
-    const u4_t w = *reinterpret_cast<const u4_t*>(q + row * (D >> 1) + blk * 16);
-    const float sc = wasm_h2f(s[row * nb + blk]);
-    const uint8_t zb = zp[row * ((nb + 1) >> 1) + (blk >> 1)];
-    const int z = (blk & 1) ? (zb >> 4) : (zb & 0xF);
-    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  const int nd = D >> 3, nb = D >> 5;
+  // 32-bit index arithmetic (the launcher checks groups * nd < 2^31): a
+  // 64-bit division is a long instruction sequence
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int groups = (T + EMB_TOK - 1) / EMB_TOK;
+  if (i >= (uint32_t)groups * (uint32_t)nd) return;
+  const int g = (int)(i / (uint32_t)nd), u = (int)(i % (uint32_t)nd);
+  const int blk = u >> 2;
+  int id[EMB_TOK];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+  for (int r = 0; r < EMB_TOK; ++r) {
+    const int t = min(g * EMB_TOK + r, T - 1);
+    id[r] = ids[t];
+  }
+  uint32_t w[EMB_TOK];
+  uint16_t sb[EMB_TOK];
+  uint8_t zb[EMB_TOK];
+#pragma unroll
+  for (int r = 0; r < EMB_TOK; ++r) {
+    const size_t row = (id[r] >= 0 && id[r] < V) ? (size_t)id[r] : 0;  // out-of-range ids read row 0, stored as 0
+    w[r] = reinterpret_cast<const uint32_t*>(q + row * (D >> 1))[u];
+    sb[r] = s[row * nb + blk];
+    zb[r] = zp[row * ((nb + 1) >> 1) + (blk >> 1)];
+  }
+#pragma unroll
+  for (int r = 0; r < EMB_TOK; ++r) {
+    const int t = g * EMB_TOK + r;
+    if (t >= T) break;
+    u4_t res = {0u, 0u, 0u, 0u};
+    if (id[r] >= 0 && id[r] < V) {
+      const float sc = wasm_h2f(sb[r]);
+      const int z = (blk & 1) ? (zb[r] >> 4) : (zb[r] & 0xF);
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = (float)((int)((wd[d] >> (4 * j)) & 0xFu) - z) * sc;
-      const u2_t a = to_f16x4(v), c = to_f16x4(v + 4);
-      res[d] = u4_t{a.x, a.y, c.x, c.y};
+      for (int j = 0; j < 8; ++j) v[j] = (float)((int)((w[r] >> (4 * j)) & 0xFu) - z) * sc;
+      const u2_t a = to_f16x4_z(v), c = to_f16x4_z(v + 4);
+      res = u4_t{a.x, a.y, c.x, c.y};
     }
+    reinterpret_cast<u4_t*>(out + (size_t)t * D)[u] = res;
   }
-  u4_t* o = reinterpret_cast<u4_t*>(out + (size_t)t * D + blk * 32);
-#pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = res[d];
 }
 
 // ----------------------------------------------------------------------------
@@ -662,7 +681,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
           yv[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)sk[k] * D + d);
         }
       }
-      rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
+      rw[j] = residual ? *reinterpret_cast<const u2_t*>(residual + base + d) : u2_t{0u, 0u};  // NULL: no residual
       if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
     }
   }
@@ -745,25 +764,57 @@ void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const 
 }
 
 // ----------------------------------------------------------------------------
-// fp16-weight router (router W fp16 [D][E], f32 accumulate,
-// bias fp16): logits[t][e] = sum_d x[t][d] W[d][e] + bias[e]. One thread per
-// (t, e); 4-lane partial sums combined as the reference's TR=8 path does.
-__global__ __launch_bounds__(128) void k_router_f16w(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                     const uint16_t* __restrict__ bias, float* __restrict__ logits,
-                                                     int T, int D, int E) {
-  extern __shared__ float xs[];
-  const int t = blockIdx.x;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) xs[d] = wasm_h2f(x[(size_t)t * D + d]);
+// fp16-weight router (router W fp16 [D][E], f32
+// accumulate, fp16 bias): logits[t][e] = sum_d x[t][d] W[d][e] + bias[e], on
+// the matrix cores. W is first transposed into wt [E][D] (a scratch copy) so
+// that every MFMA operand is one 16-byte load: A = W^T (16 experts x 32 k),
+// B = x^T (32 k x 16 tokens); a lane ends with 4 consecutive experts of one
+// token. One wave per 16 tokens and 32 experts (many small workgroups: the
+// GEMM is tiny and its K loop is a chain of L2 loads); operands come straight
+// from global memory (W^T is 160 KB and L2-resident).
+__global__ __launch_bounds__(256) void k_transpose_f16(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                       int D, int E) {
+  __shared__ uint16_t tile[32][33];
+  const int e0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    const int d = d0 + r, e = e0 + tx;
+    tile[r][tx] = (d < D && e < E) ? w[(size_t)d * E + e] : (uint16_t)0;
+  }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    float l[4] = {0.f, 0.f, 0.f, 0.f};
-    int d = 0;
-    for (; d + 4 <= D; d += 4)
+  for (int r = ty; r < 32; r += 8) {
+    const int e = e0 + r, d = d0 + tx;
+    if (e < E && d < D) wt[(size_t)e * D + d] = tile[tx][r];
+  }
+}
+
+__global__ __launch_bounds__(64) void k_router_f16w(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt,
+                                                    const uint16_t* __restrict__ bias, float* __restrict__ logits,
+                                                    int T, int D, int E) {
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int t0 = blockIdx.x * 16, eb = blockIdx.y * 32;
+  const uint16_t* arow[2];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) l[c] = fmaf(xs[d + c], wasm_h2f(w[(size_t)(d + c) * E + e]), l[c]);
-    float s = (l[0] + l[1]) + (l[2] + l[3]);
-    for (; d < D; ++d) s = fmaf(xs[d], wasm_h2f(w[(size_t)d * E + e]), s);
-    logits[(size_t)t * E + e] = s + (bias ? wasm_h2f(bias[e]) : 0.0f);
+  for (int f = 0; f < 2; ++f) arow[f] = wt + (size_t)min(eb + 16 * f + l16, E - 1) * D + 8 * lg;
+  const uint16_t* brow = x + (size_t)min(t0 + l16, T - 1) * D + 8 * lg;
+  f4_t acc[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+  for (int k = 0; k < D; k += 32) {
+    const h8_t a0 = __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(arow[0] + k));
+    const h8_t a1 = __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(arow[1] + k));
+    const h8_t bb = __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(brow + k));
+    acc[0] = mfma16x16x32(a0, bb, acc[0]);
+    acc[1] = mfma16x16x32(a1, bb, acc[1]);
+  }
+  const int t = t0 + l16;
+  if (t >= T) return;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int e = eb + 16 * f + 4 * lg;
+    float* o = logits + (size_t)t * E + e;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (e + r < E) o[r] = acc[f][r] + (bias ? hw_h2f(bias[e + r]) : 0.0f);
   }
 }
 
@@ -979,7 +1030,8 @@ void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const u
   PF_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)out & 15) == 0,
            "embed_lookup: table and output must be 16-byte aligned");
   if (T <= 0) return;
-  const size_t n = (size_t)T * (D / 32);
+  const size_t n = (size_t)((T + EMB_TOK - 1) / EMB_TOK) * (D / 8);
+  PF_CHECK(n < (1ull << 31), "embed_lookup: too many rows");
   ProfScope ps(b, "embed_lookup_int4");
   hipLaunchKernelGGL(k_embed, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, b->stream, q, s, zp, ids, out, T, V,
                      D);
@@ -1191,11 +1243,15 @@ void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, cons
 }
 
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
-                 int D, int E) {
-  PF_CHECK(D > 0 && D <= 16384 && E > 0, "router_f16w: bad shape");
+                 int D, int E, uint16_t* wt) {
+  PF_CHECK(D > 0 && D % 32 == 0 && E > 0, "router_f16w: D must be a positive multiple of 32");
+  PF_CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)wt & 15) == 0, "router_f16w: 16-byte aligned x and scratch");
   if (T <= 0) return;
   ProfScope ps(b, "router_f16w");
-  hipLaunchKernelGGL(k_router_f16w, dim3(T), dim3(128), D * sizeof(float), b->stream, x, w, bias, logits, T, D, E);
+  hipLaunchKernelGGL(k_transpose_f16, dim3((E + 31) / 32, (D + 31) / 32), dim3(256), 0, b->stream, w, wt, D, E);
+  PF_HIP(hipGetLastError());
+  hipLaunchKernelGGL(k_router_f16w, dim3((T + 15) / 16, (E + 31) / 32), dim3(64), 0, b->stream, x, wt, bias,
+                     logits, T, D, E);
   PF_HIP(hipGetLastError());
 }
 

@@ -210,15 +210,17 @@ int moe_max_tiles(int T, int K, int E, int tile_t);
 size_t moe_plan_bytes(int T, int K, int E, int tile_t);
 MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t);
 void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const MoePlan& plan);
-// y: the expert outputs in slot order, fp16 when y16 (the fp16 numerics), else f32.
+// y: the expert outputs in slot order, fp16 when y16 (the fp16 numerics), else f32;
+// residual NULL: no residual (the outputs hold the MoE result alone).
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
                  bool y16, const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, int T, int K, int D);
 // norm_lo == NULL: the norm output is one fp16 plane in norm_hi.
 void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
                       bool y16, const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps);
+// fp16-weight router GEMM (MFMA); wt: scratch for W^T, E * D fp16, 16-byte aligned.
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
-                 int D, int E);
+                 int D, int E, uint16_t* wt);
 
 // Banded GQA attention with sinks.
 struct AttnArgs {

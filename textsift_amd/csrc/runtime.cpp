@@ -170,14 +170,14 @@ static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw
   const size_t S = (size_t)T * K;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t plan_b = moe_plan_bytes(T, K, E, et.t);
-  const size_t bytes = al((size_t)T * E * 4) + al(S * F * 2) + al(S * D * 4) + al((size_t)T * D * 2) + plan_b;
+  const size_t bytes = al((size_t)T * E * 4) + al(S * F * 2) + al(S * D * 4) + plan_b + al((size_t)E * D * 2);
   char* s = static_cast<char*>(backend_scratch(b, bytes));
+  uint16_t* wt = reinterpret_cast<uint16_t*>(s); s += al((size_t)E * D * 2);
   float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
   uint16_t* glu = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
   float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
-  uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
   MoePlan m = moe_plan_carve(s, T, K, E, et.t);
-  router_f16w(b, x, rw, rb, logits, T, D, E);
+  router_f16w(b, x, rw, rb, logits, T, D, E, wt);
   router_topk(b, logits, ridx, rwt, T, E, K, 1.0f);
   moe_route(b, ridx, T, K, E, m);
   GemmArgs g;
@@ -194,9 +194,8 @@ static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw
   d.out = y; d.ldo = D; d.M = (int)S; d.N = D; d.K = F;
   d.tiles = m.tiles; d.num_tiles = m.num_tiles; d.max_tiles = m.max_tiles;
   gemm_w4(b, d, XKind::F16, Epi::F16, true, et.t, et.wf, "moe_down");  // fp16 expert outputs, as the forward
-  // out = fp16(sum_k w_k y_k) (zero residual -> the output holds the MoE output)
-  zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
-  moe_combine(b, ridx, rwt, m.slot_of, y, true, zero_res, nullptr, out, T, K, D);
+  // out = fp16(sum_k w_k y_k) (no residual: the output holds the MoE output)
+  moe_combine(b, ridx, rwt, m.slot_of, y, true, nullptr, nullptr, out, T, K, D);
 }
 
 // Dense GEMM of the fp16 forward on prepared weights, tile as the forward
@@ -565,16 +564,16 @@ static std::vector<KernelEntry>& registry() {
                  const size_t gu_w = al((size_t)E * 2 * F * D / 2), gu_s = al((size_t)E * 2 * F * (D / 32) * 4);
                  const size_t dn_w = al((size_t)E * D * F / 2), dn_s = al((size_t)E * D * (F / 32) * 4);
                  const size_t bytes = al((size_t)T * E * 4) + 2 * al(S * F * 2) + al(S * D * 4) +
-                                      2 * al((size_t)T * D * 2) + al((size_t)T * D * 2) + plan_b +
-                                      (f16 ? gu_w + gu_s + dn_w + dn_s : 0);
+                                      2 * al((size_t)T * D * 2) + plan_b +
+                                      (f16 ? gu_w + gu_s + dn_w + dn_s : 0) + al((size_t)E * D * 2);
                  char* s = static_cast<char*>(backend_scratch(b, bytes));
+                 uint16_t* wt = reinterpret_cast<uint16_t*>(s); s += al((size_t)E * D * 2);
                  float* logits = reinterpret_cast<float*>(s); s += al((size_t)T * E * 4);
                  uint16_t* glu_hi = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
                  uint16_t* glu_lo = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
                  float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
                  uint16_t* x_hi = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  uint16_t* x_lo = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
-                 uint16_t* zero_res = reinterpret_cast<uint16_t*>(s); s += al((size_t)T * D * 2);
                  MoePlan m = moe_plan_carve(s, T, K, E, tt); s += plan_b;
                  // activations: f32 input -> hi/lo planes; an fp16 input is exact as one plane
                  const XKind xk = xf32 ? XKind::SPLIT : XKind::F16;
@@ -594,7 +593,7 @@ static std::vector<KernelEntry>& registry() {
                  } else {
                    PF_CHECK(!xf32, "moe_ffn: the fp16-weight router takes fp16 activations");
                    need(bs, 1, (size_t)D * E * 2, "moe_ffn");
-                   router_f16w(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 4), logits, T, D, E);
+                   router_f16w(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 4), logits, T, D, E, wt);
                  }
                  router_topk(b, logits, bp<int32_t>(bs, 14), bp<float>(bs, 15), T, E, K, 1.0f);
                  moe_route(b, bp<int32_t>(bs, 14), T, K, E, m);
@@ -632,9 +631,8 @@ static std::vector<KernelEntry>& registry() {
                    gemm_int4(b, g, xk, Epi::SWIGLU_SPLIT, true, tt, "moe_gate_up");
                    gemm_int4(b, d, XKind::SPLIT, Epi::F32, true, tt, "moe_down");
                  }
-                 // out = fp16(sum_k w_k y_k) (zero residual -> h_out holds the MoE output)
-                 zero_f32(b, reinterpret_cast<float*>(zero_res), ((size_t)T * D * 2 + 3) / 4);
-                 moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, f16, zero_res, nullptr,
+                 // out = fp16(sum_k w_k y_k) (no residual: h_out holds the MoE output)
+                 moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, f16, nullptr, nullptr,
                              bp<uint16_t>(bs, 13), T, K, D);
                }});
   r.push_back({"probe_mfma_f16", 3, 0, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*) {
