@@ -629,7 +629,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
 // than the general 4, so more waves stay resident).
 // Y16: the expert outputs are fp16 (the fp16 numerics' down GEMM rounds them
 // once; widened here by the hardware), else f32.
-template <int NMODE, int K, int NJ = MAXJ, bool Y16 = false>
+template <int NMODE, int K, int NJ = MAXJ, bool Y16 = false, bool RES = true>
 __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__ idx, const float* __restrict__ w,
                                                      const int32_t* __restrict__ slot_of, const void* __restrict__ y,
                                                      const uint16_t* __restrict__ residual,
@@ -681,7 +681,8 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
           yv[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)sk[k] * D + d);
         }
       }
-      rw[j] = residual ? *reinterpret_cast<const u2_t*>(residual + base + d) : u2_t{0u, 0u};  // NULL: no residual
+      if constexpr (RES) rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
+      else rw[j] = u2_t{0u, 0u};
       if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
     }
   }
@@ -731,29 +732,23 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
   }
 }
 
-template <int NMODE>
-void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
-                    bool y16, const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
-                    uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
+template <int NMODE, bool Y16, bool RES>
+void launch_combine_t(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
+                      const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
+                      uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
   const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
-  if (y16) {  // the fp16 numerics (the model's K = 4, or any K up to 8 on 4 slices)
+  if (Y16 || (D <= 768 && K == 4)) {  // the model's shape (fp16 expert outputs are built for it only)
     PF_CHECK(K == 4 && D <= 768, "moe_combine: fp16 expert outputs are built for K = 4, D <= 768");
-    hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3, true>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y,
+    hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3, Y16, RES>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y,
                        residual, moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);
     PF_HIP(hipGetLastError());
     return;
   }
-  if (D <= 768 && K == 4) {  // the model's shape
-    hipLaunchKernelGGL((k_moe_combine<NMODE, 4, 3>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y, residual,
-                       moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);
-    PF_HIP(hipGetLastError());
-    return;
-  }
   switch (K) {
-#define PF_COMBINE_CASE(k)                                                                                       \
-  case k:                                                                                                        \
-    hipLaunchKernelGGL((k_moe_combine<NMODE, k>), grid, dim3(256), 0, b->stream, idx, w, slot_of, y, residual,   \
-                       moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);                                      \
+#define PF_COMBINE_CASE(k)                                                                                         \
+  case k:                                                                                                          \
+    hipLaunchKernelGGL((k_moe_combine<NMODE, k, MAXJ, false, RES>), grid, dim3(256), 0, b->stream, idx, w, slot_of, \
+                       y, residual, moe_out, h_out, gamma, norm_hi, norm_lo, T, D, eps);                           \
     break;
     PF_COMBINE_CASE(1) PF_COMBINE_CASE(2) PF_COMBINE_CASE(3) PF_COMBINE_CASE(4)
     PF_COMBINE_CASE(5) PF_COMBINE_CASE(6) PF_COMBINE_CASE(7) PF_COMBINE_CASE(8)
@@ -761,6 +756,28 @@ void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const 
     default: throw Error("moe_combine: K must be 1..8");
   }
   PF_HIP(hipGetLastError());
+}
+
+// residual NULL: no residual (a variant that loads none)
+template <int NMODE>
+void launch_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
+                    bool y16, const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
+                    uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
+  if (y16) {
+    if (residual)
+      launch_combine_t<NMODE, true, true>(b, idx, w, slot_of, y, residual, moe_out, h_out, gamma, norm_hi, norm_lo, T,
+                                          K, D, eps);
+    else
+      launch_combine_t<NMODE, true, false>(b, idx, w, slot_of, y, residual, moe_out, h_out, gamma, norm_hi, norm_lo,
+                                           T, K, D, eps);
+  } else {
+    if (residual)
+      launch_combine_t<NMODE, false, true>(b, idx, w, slot_of, y, residual, moe_out, h_out, gamma, norm_hi, norm_lo,
+                                           T, K, D, eps);
+    else
+      launch_combine_t<NMODE, false, false>(b, idx, w, slot_of, y, residual, moe_out, h_out, gamma, norm_hi, norm_lo,
+                                            T, K, D, eps);
+  }
 }
 
 // ----------------------------------------------------------------------------
