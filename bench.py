@@ -216,6 +216,21 @@ def sq_report(p1_csv, p2_csv, cus=256, ses=32):
     return "\n".join(lines)
 
 
+def stats_report(stats_csv, top=20):
+    """Markdown table of a rocprofv3 --stats kernel_stats.csv: per kernel
+    symbol, calls and average/min/max duration, by total time."""
+    import csv
+    with open(stats_csv, newline="") as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    lines = ["| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        name = r["Name"] if len(r["Name"]) <= 100 else r["Name"][:97] + "..."
+        lines.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                     f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    return "\n".join(lines)
+
+
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed traffic summary, or None."""
     path = os.path.join(ROOT, "profiles", "forward_16x2048_hbm_traffic.md")
@@ -720,6 +735,7 @@ def main():
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--copy-mb", type=int, default=1024)
     ap.add_argument("--raw-symbols", action="store_true", help="--traffic-report: group by kernel symbol")
+    ap.add_argument("--stats-report", metavar="KERNEL_STATS_CSV", help="markdown table of a rocprofv3 --stats csv")
     ap.add_argument("--variant", choices=["both", "warm", "cold"], default="both",
                     help="--config 1-4: which cache variants to time (one alone for rocprofv3 runs)")
     ap.add_argument("--sq-report", nargs=2, metavar=("PASS1_CSV", "PASS2_CSV"),
@@ -747,6 +763,9 @@ def main():
 
     if args.traffic_report:
         print(traffic_report(args.traffic_report[0], args.traffic_report[1], args.copy_mb, raw=args.raw_symbols))
+        return
+    if args.stats_report:
+        print(stats_report(args.stats_report))
         return
     if args.sq_report:
         print(sq_report(args.sq_report[0], args.sq_report[1]))

@@ -141,10 +141,10 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int any_hi = wave_max_i(q_ok ? hi0 : 0);
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
-  const int GH = G / a.head_groups;          // query heads per workgroup
   const float sscale = a.scale;
 
-  for (int hh = hgrp * GH; hh < (hgrp + 1) * GH; ++hh) {
+  // this workgroup's query heads: an even split of the group's G heads
+  for (int hh = hgrp * G / a.head_groups; hh < (hgrp + 1) * G / a.head_groups; ++hh) {
     const int hq = g * G + hh;
     // Opaque per-head copies of the window bounds: comparisons against them
     // are then recomputed per head instead of being hoisted out of the loop
@@ -338,11 +338,11 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   auto empty = [&](int c) { return 32 * c + 32 <= any_lo || 32 * c >= any_hi; };
   const bool masked = a.mask != nullptr;
   const int G = a.Hq / a.Hkv;
-  const int GH = G / a.head_groups;          // query heads per workgroup
   constexpr float LOG2_E = 1.44269504088896340736f;
   const float sscale = a.scale * LOG2_E;     // scores in the exponent's units
 
-  for (int hh = hgrp * GH; hh < (hgrp + 1) * GH; ++hh) {
+  // this workgroup's query heads: an even split of the group's G heads
+  for (int hh = hgrp * G / a.head_groups; hh < (hgrp + 1) * G / a.head_groups; ++hh) {
     const int hq = g * G + hh;
     // opaque per-head copies of the window bounds (see k_banded_attention)
     int lo = lo0, hi = hi0;
@@ -509,11 +509,13 @@ void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, size_t lds, 
                                (int)lds));
     attr_set = true;
   }
-  // few workgroups (short inputs): one per query head instead of one per KV
-  // head group, so the heads run in parallel
+  // few workgroups (short inputs): the query heads of a KV head are split
+  // over several workgroups (the fewest that give every CU one), so they run
+  // in parallel; each still stages its K/V rows once for all its heads
   AttnArgs g = a;
   const long wgs = (long)((a.T + qb - 1) / qb) * a.Hkv * a.B;
-  g.head_groups = wgs < b->num_cus ? a.Hq / a.Hkv : 1;
+  const int G = a.Hq / a.Hkv;
+  g.head_groups = (int)std::min<long>(G, (b->num_cus + wgs - 1) / wgs);
   dim3 grid((a.T + qb - 1) / qb, a.Hkv * g.head_groups, a.B);
   ProfScope ps(b, "banded_attention");
   hipLaunchKernelGGL(kern, grid, dim3(nt), lds, b->stream, g);

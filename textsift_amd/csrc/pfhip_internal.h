@@ -233,7 +233,7 @@ struct AttnArgs {
   int B, T, Hq, Hkv, head_dim, window;
   float scale;
   int hw_exp;           // 1: hardware exp2 softmax (the GPU paths' numerics); 0: the WASM path's
-  int head_groups = 1;  // set by the launcher: workgroups per KV head (each takes Hq/Hkv/head_groups heads)
+  int head_groups = 1;  // set by the launcher: workgroups per KV head (an even split of its Hq/Hkv query heads)
 };
 void banded_attention(pfhip_backend* b, const AttnArgs& a);
 
