@@ -482,7 +482,7 @@ static std::vector<KernelEntry>& registry() {
                }});
   // moe_ffn_w4: moe_ffn in the fp16 numerics on prepared expert weights (BASELINE config 3 as the
   // forward runs it). push {T, D, E, K, dff, tile_t, wf, 0} (tile_t 0: the forward's expert tile;
-  // else one of gemm_w4's tiles: (256, 4), (128, 4), (64, 5), (16, 1)); bindings [x fp16 [T][D], router_w fp16 [D][E],
+  // else one of gemm_w4's grouped tiles: (128, 4), (64, 5), (64, 1), (16, 1)); bindings [x fp16 [T][D], router_w fp16 [D][E],
   // router_bias fp16 [E], gu.w4, gu.sz, gu.bias, dn.w4, dn.sz, dn.bias, out fp16 [T][D], routing_idx [T][K],
   // routing_w [T][K]]
   r.push_back({"moe_ffn_w4", 12, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {

@@ -148,10 +148,14 @@ def make_model_weights(cfg: ModelConfig = PF_CONFIG, seed: int = 20260101, *, nu
     return w
 
 
-def zipf_router(seed: int, d: int, e: int, s: float = 1.1, strength: float = 0.35):
+def zipf_router(seed: int, d: int, e: int, s: float = 1.1, strength: float = 0.32):
     """BASELINE config 3's router: fp16 W [d][e] ~ N(0, 0.02) and an fp16
     bias of -s * strength * ln(rank) (rank = expert id + 1), which skews the
-    realised top-k load towards Zipf(s). Returns (W bits [d][e], bias bits [e])."""
+    realised top-k load towards Zipf(s). strength 0.32 is calibrated for
+    d = 640, e = 128, top-4 over 2048 N(0, 1) rows: a log-log fit over the 32
+    most-loaded experts gives s = 1.10, and the 8 most-loaded take 58 % of
+    the assignments (Zipf(1.1) over 128 ranks: 57 %).
+    Returns (W bits [d][e], bias bits [e])."""
     w = to_fp16_bits(normal(seed, d * e, 0, 0.02)).reshape(d, e)
     bias = to_fp16_bits(s * -np.log(np.arange(1, e + 1)) * strength)
     return w, bias
