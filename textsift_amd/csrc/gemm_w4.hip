@@ -190,13 +190,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     xoff[m] = g * p.ldx + ((l16 ^ (r & 15)) << 3);
   }
 
+  // (byte offsets as unsigned 32-bit values from a uniform base: the loads
+  // take the scalar-base + 32-bit-offset form, no 64-bit address arithmetic)
   auto load_x = [&](int c, int buf) {
 #pragma unroll
     for (int pl = 0; pl < XS; ++pl)
 #pragma unroll
       for (int m = 0; m < XI; ++m) {
         _Float16* dst = xs_lds + (buf * XS + pl) * PLANE + (m * NW + wave) * 512;
-        copy16_to_lds(xsrc[pl] + xoff[m] + c * KC, (lds_ptr_t)dst);
+        copy16_to_lds(reinterpret_cast<const char*>(xsrc[pl]) + (uint32_t)(xoff[m] + c * KC) * 2u, (lds_ptr_t)dst);
       }
   };
 
@@ -212,7 +214,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 
   // The accumulators start at the bias of the lane's 4 columns of each
   // fragment (the MFMAs add onto it); columns past N get 0 and are never
-  // stored. Loads are unconditional (indices clamped).
+  // stored. Loads are unconditional (indices clamped). The bias widens with
+  // the hardware conversion (this GEMM serves the fp16 numerics, the GPU
+  // shaders' arithmetic).
   const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
   int ncol[WF];
 #pragma unroll
@@ -242,7 +246,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       float bv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        bv[r] = ncol[f] + r < p.N ? wasm_h2f((uint16_t)(bw[r >> 1] >> (16 * (r & 1)))) : 0.0f;
+        bv[r] = ncol[f] + r < p.N ? (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[r >> 1] >> (16 * (r & 1))))
+                                  : 0.0f;
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
     }
@@ -895,7 +900,7 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
       const u2_t bw = *reinterpret_cast<const u2_t*>(p.bias + ncol[f]);
       const uint32_t bwv[2] = {bw.x, bw.y};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bv[r] = wasm_h2f((uint16_t)(bwv[r >> 1] >> (16 * (r & 1))));
+      for (int r = 0; r < 4; ++r) bv[r] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bwv[r >> 1] >> (16 * (r & 1))));
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
