@@ -298,7 +298,18 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 // keeps f32 weights; the fp16 weight is this path's one extra rounding
 // (output error ~3e-4 relative against the shader's f32 weights). Requires
 // scale > 0 (the row maximum is taken over the unscaled scores).
-template <int HD, int NCH, int NW>
+// max(a, b, c) in one v_max3_f32. Written as assembly: the compiler's
+// fmaxf quiets each operand first (signalling NaNs), which MFMA results and
+// -inf never are.
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// MASKED: a key mask is given (a compile-time choice, so the unmasked
+// kernel carries no per-slot mask code)
+template <int HD, int NCH, int NW, bool MASKED>
 __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   using GE = AttnGeom<HD, NCH, NW>;
   constexpr int QB = 16 * NW;                // query tokens per workgroup
@@ -336,7 +347,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   const int any_lo = wave_min_i(q_ok ? lo0 : 1 << 20);
   const int any_hi = wave_max_i(q_ok ? hi0 : -1);
   auto empty = [&](int c) { return 32 * c + 32 <= any_lo || 32 * c >= any_hi; };
-  const bool masked = a.mask != nullptr;
+  constexpr bool masked = MASKED;
   const int G = a.Hq / a.Hkv;
   constexpr float LOG2_E = 1.44269504088896340736f;
   const float sscale = a.scale * LOG2_E;     // scores in the exponent's units
@@ -358,8 +369,11 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
 
     // ---- pass 1: unscaled scores for the whole band, kept in registers;
     // slots outside the query's window and masked keys hold -inf. The K
-    // fragments of chunk c + 1 are read while chunk c is processed.
-    float s[NCH][2][4];
+    // fragments of chunk c + 1 are read while chunk c is processed. The
+    // MFMAs write the score registers themselves and edge chunks are masked
+    // in place (no copies between register sets); the running maximum takes
+    // three values per instruction.
+    f4_t s[NCH][2];
     float mr = -INFINITY;
     // K fragments double-buffered by chunk parity (compile-time indices once
     // the chunk loop is unrolled: no register copies between chunks)
@@ -376,39 +390,32 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     for (int c = 0; c < NCH; ++c) {
       if (c + 1 < NCH) load_k(c + 1, kb[(c + 1) & 1]);
       const h8_t (&kf)[2][NDH] = kb[c & 1];
-      f4_t acc[2];
-      if (!empty(c)) {
+      if (empty(c)) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][0], qf[0], f4_t{0.f, 0.f, 0.f, 0.f});
+        for (int kt = 0; kt < 2; ++kt) s[c][kt] = f4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[c][kt] = mfma16x16x32(kf[kt][0], qf[0], f4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int dh = 1; dh < NDH; ++dh)
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt) acc[kt] = mfma16x16x32(kf[kt][dh], qf[dh], acc[kt]);
-      }
-      if (empty(c)) {
+          for (int kt = 0; kt < 2; ++kt) s[c][kt] = mfma16x16x32(kf[kt][dh], qf[dh], s[c][kt]);
+        if (masked || 32 * c < full_lo || 32 * c + 32 > full_hi) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+          for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s[c][kt][r] = -INFINITY;
-      } else if (!masked && 32 * c >= full_lo && 32 * c + 32 <= full_hi) {
+            for (int r = 0; r < 4; ++r) {
+              const int off = 32 * c + 16 * kt + 4 * lg + r;
+              bool valid = (off >= lo) & (off < hi);
+              if constexpr (MASKED) valid = valid && a.mask[seq0 + kw + off] != 0;
+              s[c][kt][r] = valid ? s[c][kt][r] : -INFINITY;
+            }
+        }
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s[c][kt][r] = acc[kt][r];
-          mr = fmaxf(mr, fmaxf(fmaxf(acc[kt][0], acc[kt][1]), fmaxf(acc[kt][2], acc[kt][3])));
+          mr = max3_f32(mr, s[c][kt][0], s[c][kt][1]);
+          mr = max3_f32(mr, s[c][kt][2], s[c][kt][3]);
         }
-      } else {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int off = 32 * c + 16 * kt + 4 * lg + r;
-            bool valid = (off >= lo) & (off < hi);
-            if (masked) valid = valid && a.mask[seq0 + kw + off] != 0;
-            const float sv = valid ? acc[kt][r] : -INFINITY;
-            s[c][kt][r] = sv;
-            mr = fmaxf(mr, sv);
-          }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -527,8 +534,13 @@ void launch_attn(pfhip_backend* b, const AttnArgs& a) {
   constexpr size_t LDS = AttnGeom<HD, NCH, NW>::LDS;
   static_assert(LDS <= 160 * 1024, "attention tile exceeds the LDS");
   if (a.hw_exp) {
-    static bool attr_set = false;
-    launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW>, LDS, 16 * NW, 64 * NW, attr_set);
+    if (a.mask) {
+      static bool attr_set = false;
+      launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, true>, LDS, 16 * NW, 64 * NW, attr_set);
+    } else {
+      static bool attr_set = false;
+      launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, false>, LDS, 16 * NW, 64 * NW, attr_set);
+    }
   } else {
     static bool attr_set = false;
     launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, LDS, 16 * NW, 64 * NW, attr_set);
