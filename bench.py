@@ -732,6 +732,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--precision", choices=["fp16", "split"], default="fp16",
+                    help="numerics of the forward: fp16 (the reference's GPU paths, the default) or split (its WASM path)")
     ap.add_argument("--profile-steps", type=int, default=2, help="steps of the all-kernel profiled pass")
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     ap.add_argument("--traffic-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
@@ -794,7 +796,8 @@ def main():
     gen_s = time.time() - t_gen
 
     be = _native.Backend(0)
-    model = _native.Model(be, cfg)
+    prec = _native.PRECISION_FP16 if args.precision == "fp16" else _native.PRECISION_SPLIT
+    model = _native.Model(be, cfg, precision=prec)
     for name, arr in weights.items():
         model.set_weight(name, arr)
     model.finalize()
@@ -904,8 +907,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4w/fp16-mfma/f32-acc",
-        "precision": "fp16 (PFHIP_PRECISION_FP16: fp16 GEMM inputs, block scale folded into fp16 weights)",
+        "dtype": "int4w/fp16-mfma/f32-acc" if args.precision == "fp16" else "int4w/f32-as-fp16x2-mfma/f32-acc",
+        "precision": ("fp16 (PFHIP_PRECISION_FP16: fp16 GEMM inputs, block scale folded into fp16 weights)"
+                      if args.precision == "fp16" else
+                      "split (PFHIP_PRECISION_SPLIT: f32 GEMM inputs as hi/lo fp16 planes, per-block f32 scaling)"),
         "data": "synthetic (seeded random-init int4 weights, uniform token ids)",
         "config": {"workload": "full synthetic 8-layer int4 MoE encoder forward (BASELINE config 5)",
                    "batch": B, "seq_len": T, "layers": cfg.num_layers, "experts": cfg.num_experts,
