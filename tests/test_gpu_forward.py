@@ -171,7 +171,7 @@ def test_full_batch_16x2048(full_ref, precision):
     """The benchmarked launch set (BASELINE config 5 at its stated batch):
     16 sequences x 2048 tokens in one forward, i.e. 32768 rows, where the
     forward takes the fused O + residual + RMSNorm kernel, the router GEMM's
-    128-row top-4 tile and 128-row expert tiles. Sequence 0 carries full_ref's
+    64-row top-4 tile and 128-row expert tiles. Sequence 0 carries full_ref's
     ids and sequence 15 is checked against its own oracle forward: rel-err
     < 2e-3, argmax agreement >= 99.9 %, identical spans. Every sequence's
     logits also equal those of its own single-sequence forward (2048 rows:

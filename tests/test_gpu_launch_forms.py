@@ -1,6 +1,6 @@
 """GPU parity of the kernel forms the 16 x 2048 forward launches that the
 smaller tests would not reach: the router GEMM's top-4 epilogue on its
-128-row tile, the fp16 grouped expert GEMMs (SwiGLU and down, scale-folded
+64- and 128-row tiles, the fp16 grouped expert GEMMs (SwiGLU and down, scale-folded
 weights) on each of their three tiles, the reference fixtures of the
 qmoe_gate_up / qmoe_down_scatter / zero_f32 kernels, and the forward's
 row-limit check. All calls go through the C ABI by kernel name."""
@@ -40,13 +40,13 @@ def run(be, name, inputs, outs, pushb):
 
 # ---------------------------------------------------------------- router GEMM + top-4 epilogue
 
-@pytest.mark.parametrize("tile,T", [(128, 1000), (128, 129), (16, 300), (16, 5)])
+@pytest.mark.parametrize("tile,T", [(128, 1000), (128, 129), (64, 1000), (64, 37), (16, 300), (16, 5)])
 @pytest.mark.parametrize("kind", ["random", "ties", "nan"])
 def test_router_topk_epilogue_bit_exact(be, kind, tile, T):
     """The router GEMM's fused top-4 + softmax (zig/wasm_exports.zig:367-426,
-    919-958) on both row tiles the forward selects: 128 rows (two threads per
-    row, insertion + rank merge; the forward's form from 16384 rows on) and
-    16 rows (sorting networks). Expert ids and weights must equal the
+    919-958) on its row tiles: 64 rows (four threads per row, insertion + rank
+    merge; the forward's form from 16384 rows on), 128 rows (two threads per
+    row) and 16 rows (sorting networks). Expert ids and weights must equal the
     oracle's insertion top-k and softmax of the logits the same launch wrote.
     "ties": every nibble at its zero-point, so each logit is its fp16 bias,
     rounded to integers (many exact ties within and across the segments the

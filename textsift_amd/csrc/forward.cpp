@@ -461,7 +461,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
         }
-        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D, 8 * SMALL_M) ? 16 : 128, 2,
+        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D, 8 * SMALL_M) ? 16 : 64, 2,
                 "gemm_router");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");

@@ -673,7 +673,7 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
       if constexpr (ALL) return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED, NW, CT>(b, a, name);
       break;
     case Epi::F32_TOPK:
-      if constexpr (WF == 2 && (BT == 128 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4)
+      if constexpr (WF == 2 && (BT == 128 || BT == 64 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4)
         return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT>(b, a, name);
       break;
   }
@@ -776,13 +776,15 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   }
   PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
   if (epi == Epi::F32_TOPK)
-    PF_CHECK(!grouped && (tile_t == 128 || tile_t == 16) && wf == 2 && a.N == 128 && a.topk_k == 4 && a.topk_idx &&
+    PF_CHECK(!grouped && (tile_t == 128 || tile_t == 64 || tile_t == 16) && wf == 2 && a.N == 128 && a.topk_k == 4 &&
+                 a.topk_idx &&
                  a.topk_w && g.out_staged,
              "gemm_w4: the top-k epilogue needs N == 128, K == 4, a 128- or 16-token tile of 128 columns and "
              "16-byte aligned f32 rows");
   if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);
+  if (tile_t == 64 && wf == 2) return dispatch_grouped<2, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 1) return dispatch_grouped<1, 64>(b, g, epi, grouped, prof_name);
   if (a.nrm_res)
     PF_CHECK(a.nrm_gamma && a.nrm_h && a.nrm_xn && a.ldx == a.K && tile_t == 16 &&

@@ -408,13 +408,13 @@ static std::vector<KernelEntry>& registry() {
                  gemm_w4(b, a, XKind::F16, out_f32 ? Epi::F32 : Epi::F16, false, tile_t, wf, "matmul_int4_w4");
                }});
   // matmul_int4_w4_topk: the router GEMM of the fp16 forward with its top-4 + softmax epilogue
-  // (gemm_w4 F32_TOPK; N == 128 experts, k == 4). push {T, N, K, tile_t} (tile_t 128 or 16, the two
+  // (gemm_w4 F32_TOPK; N == 128 experts, k == 4). push {T, N, K, tile_t} (tile_t 128, 64 or 16, the
   // row tiles the forward selects by row count); bindings [x fp16, w, scales, zp, bias, logits f32 [T][N],
   // routing_idx i32 [T][4], routing_w f32 [T][4]]
   r.push_back({"matmul_int4_w4_topk", 8, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), N = (int)pu(p, 1), K = (int)pu(p, 2), tile_t = (int)pu(p, 3);
-                 PF_CHECK(N == 128 && K % 128 == 0 && (tile_t == 128 || tile_t == 16),
-                          "matmul_int4_w4_topk: N must be 128, K a multiple of 128 and tile_t 128 or 16");
+                 PF_CHECK(N == 128 && K % 128 == 0 && (tile_t == 128 || tile_t == 64 || tile_t == 16),
+                          "matmul_int4_w4_topk: N must be 128, K a multiple of 128 and tile_t 128, 64 or 16");
                  const int nb = K / 32;
                  need(bs, 0, (size_t)T * K * 2, "matmul_int4_w4_topk");
                  need(bs, 1, (size_t)N * K / 2, "matmul_int4_w4_topk");
