@@ -232,9 +232,11 @@ def test_matmul_w4_tiles_bit_identical(be, N, K):
         assert np.array_equal(o, base), f"tile {k} differs from (128, 4)"
 
 
-@pytest.mark.parametrize("tile_t,wf", [(64, 5), (16, 1)])
-def test_matmul_w4_fp16_out(be, tile_t, wf):
-    T, N, K = 70, 640, 640
+@pytest.mark.parametrize("tile_t,wf,N", [(64, 5, 640), (16, 1, 640), (128, 4, 640), (128, 4, 1152)])
+def test_matmul_w4_fp16_out(be, tile_t, wf, N):
+    """fp16 output = the f32 output rounded, on the tiles the forward uses
+    (N = 640: down and O; N = 1152: QKV)."""
+    T, K = 70, 640
     w = synth.qweight(77, N, K, zp=8)
     x = synth.to_fp16_bits(synth.normal(78, T * K)).reshape(T, K)
     o32 = run(be, "matmul_int4_w4", [x, w["int4"], w["scales"], w["zp"], w["bias"]], T * N * 4,

@@ -819,6 +819,14 @@ constexpr int RN_BN = RN_NW * RN_WF * 16;  // 640
 // weight sets and addresses exceed 256 and spill.)
 constexpr int RN_PD = RN_BT <= 64 ? 2 : 1;
 constexpr int RN_NB = RN_PD + 1;
+// The residual tile (BT rows x 640 fp16) is copied into LDS behind the
+// activation buffers while the last chunks are computed: RN_RESC 16-byte
+// copies per lane, rows of 80 units whose unit u sits at slot u ^ (row & 15)
+// (XOR within aligned 16-unit blocks, so the 16 rows a wave reads at once
+// fall in distinct banks).
+constexpr int RN_RESC = RN_BT * RN_BN * 2 / 16 / (64 * RN_NW);
+static_assert(RN_BT * RN_BN * 2 % (16 * 64 * RN_NW) == 0 && RN_BN % 128 == 0, "whole residual copies");
+constexpr size_t RN_LDS = (size_t)RN_NB * RN_BT * KC * 2 + (size_t)RN_BT * RN_BN * 2;
 
 // copy16_to_lds issued as inline assembly: the compiler then does not know
 // that it writes LDS and does not make every workgroup barrier wait for all
@@ -845,7 +853,11 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   // WF weight and WF scale loads, then XI activation copies
   constexpr int VM_PER_CHUNK = 2 * WF + XI;
   constexpr int PD = RN_PD, NB = RN_NB;
-  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [NB][BT][KC] swizzled, then the row sums
+  // the residual copies are issued in chunk C0's iteration, after the last chunk's loads
+  constexpr int C0 = C - 1 - PD;
+  static_assert(C0 >= 0, "residual copies after the last chunk's loads");
+  // [NB][BT][KC] swizzled activations (then the row sums), then [BT][640] residual
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -879,6 +891,17 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     for (int m = 0; m < XI; ++m)
       copy16_to_lds_async(xsrc + xoff[m] + c * KC,
                           __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(buf * PLANE + (m * NW8 + wave) * 512) * 2));
+  };
+  const uint32_t res_lds = lds0 + (uint32_t)(NB * PLANE) * 2;
+  auto load_res_lds = [&]() {
+#pragma unroll
+    for (int i = 0; i < RN_RESC; ++i) {
+      const int u = (i * NW8 + wave) * 64 + lane;  // LDS unit of this lane's copy
+      const int t = u / (RN_BN / 8), slot = u % (RN_BN / 8);
+      const int g = slot ^ (t & 15);               // the row's unit held there
+      copy16_to_lds_async(resid + (size_t)(row0 + min(t, rows - 1)) * RN_BN + g * 8,
+                          __builtin_amdgcn_readfirstlane(res_lds + (uint32_t)((i * NW8 + wave) * 64) * 16));
+    }
   };
   u4_t wraw[C][WF];  // only PD + 1 chunks' sets are live at a time
   uint32_t sz[C][WF];
@@ -947,9 +970,16 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     // instructions are outstanding than were issued after them: those of
     // chunks c + 1 .. c + PD - 1 (s_waitcnt: vmcnt in bits 3:0 and 15:14;
     // expcnt and lgkmcnt at their maxima, i.e. not waited on).
-    static_assert(VM_PER_CHUNK < 64 && PD <= 2, "vmcnt is 6 bits");
-    if (PD == 2 && c + 1 < C) {
+    // The residual copies, issued after chunk C - 1's loads, may stay in
+    // flight until the epilogue.
+    static_assert(VM_PER_CHUNK + RN_RESC < 64 && PD <= 2, "vmcnt is 6 bits");
+    constexpr int VR = VM_PER_CHUNK + RN_RESC;
+    if (PD == 2 && c + 1 < C && c <= C0) {
       __builtin_amdgcn_s_waitcnt((VM_PER_CHUNK & 15) | (7 << 4) | (15 << 8) | ((VM_PER_CHUNK >> 4) << 14));
+    } else if (PD == 2 && c + 1 < C) {
+      __builtin_amdgcn_s_waitcnt((VR & 15) | (7 << 4) | (15 << 8) | ((VR >> 4) << 14));
+    } else if (c > C0) {
+      __builtin_amdgcn_s_waitcnt((RN_RESC & 15) | (7 << 4) | (15 << 8) | ((RN_RESC >> 4) << 14));
     } else {
       __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     }
@@ -963,9 +993,15 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
       load_w(c + PD);
       load_x(c + PD, (c + PD) % NB);
     }
+    if (c == C0) load_res_lds();
     compute(c);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // every wave's residual copies have landed
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
   // ---- epilogue: lane holds o[token 16 tj + l16][ncol[f] .. + 3]
   u2_t gw[WF];
@@ -973,13 +1009,31 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   for (int f = 0; f < WF; ++f) gw[f] = *reinterpret_cast<const u2_t*>(gamma + ncol[f]);
   u2_t hs[WF][TJ];   // h2 (fp16)
   float ss[TJ];
-  // residual rows one token fragment ahead (all at once would not fit the registers)
+  // residual rows from LDS, one token fragment ahead
+  // (h2, then xn, are written over the residual in the same layout and
+  // leave as whole rows)
+  char* res_tile = reinterpret_cast<char*>(xs_lds) + NB * PLANE * 2;
+  auto res_at = [&](int tj, int f) -> u2_t* {
+    const int t = 16 * tj + l16;  // rows past the tile hold copies of the last (never stored)
+    const int u = ncol[f] >> 3;   // 16-byte unit; the lane's 8 bytes are its half 4 lg & 4
+    return reinterpret_cast<u2_t*>(res_tile + t * (RN_BN * 2) + ((u ^ (t & 15)) << 4) + (ncol[f] & 4) * 2);
+  };
   u2_t rres[2][WF];
   auto load_res = [&](int tj, u2_t (&dst)[WF]) {
-    const int t = min(16 * tj + l16, rows - 1);  // rows past the tile repeat the last (never stored)
 #pragma unroll
-    for (int f = 0; f < WF; ++f)
-      dst[f] = *reinterpret_cast<const u2_t*>(resid + (size_t)(row0 + t) * RN_BN + ncol[f]);
+    for (int f = 0; f < WF; ++f) dst[f] = *res_at(tj, f);
+  };
+  // the tile's rows from LDS to dst: unit slot U of the tile is unit
+  // (U % 80) ^ (row & 15) of row U / 80
+  auto store_rows = [&](uint16_t* __restrict__ dst) {
+#pragma unroll
+    for (int i = 0; i < RN_RESC; ++i) {
+      const int U = i * 64 * NW8 + tid;
+      const int t = U / (RN_BN / 8), slot = U % (RN_BN / 8);
+      if (t < rows)
+        *reinterpret_cast<u4_t*>(dst + (size_t)(row0 + t) * RN_BN + (slot ^ (t & 15)) * 8) =
+            *reinterpret_cast<const u4_t*>(res_tile + U * 16);
+    }
   };
   load_res(0, rres[0]);
 #pragma unroll
@@ -998,12 +1052,13 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
         ss[tj] = fmaf(sv[r], sv[r], ss[tj]);
       }
       hs[f][tj] = to_f16x4_native(sv);
+      *res_at(tj, f) = hs[f][tj];  // over the residual this lane read
     }
     __builtin_amdgcn_sched_barrier(0);
   }
   // row sums of squares: the 4 lane groups, then the 8 waves (fixed order)
   float* red = reinterpret_cast<float*>(xs_lds);  // [NW8][BT]
-  __syncthreads();  // every wave is done with the activation buffers
+  __syncthreads();  // every wave is done with the activation buffers, and h2 is in LDS
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj) {
     float v = ss[tj];
@@ -1011,7 +1066,8 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     v += __shfl_xor(v, 32, 64);
     if (lg == 0) red[wave * BT + 16 * tj + l16] = v;
   }
-  __syncthreads();
+  store_rows(h_out);
+  __syncthreads();  // the row sums are written and every h2 unit is read
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj) {
     const int t = 16 * tj + l16;
@@ -1019,20 +1075,18 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
 #pragma unroll
     for (int w = 0; w < NW8; ++w) tot += red[w * BT + t];
     const float inv_rms = 1.0f / sqrtf(tot * (1.0f / (float)RN_BN) + eps);
-    if (t < rows) {
-      const size_t base = (size_t)(row0 + t) * RN_BN;
 #pragma unroll
-      for (int f = 0; f < WF; ++f) {
-        const h4_t hv = __builtin_bit_cast(h4_t, hs[f][tj]);
-        const h4_t gm = __builtin_bit_cast(h4_t, gw[f]);
-        float y[4];
+    for (int f = 0; f < WF; ++f) {
+      const h4_t hv = __builtin_bit_cast(h4_t, hs[f][tj]);
+      const h4_t gm = __builtin_bit_cast(h4_t, gw[f]);
+      float y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = (float)hv[r] * inv_rms * (float)gm[r];
-        *reinterpret_cast<u2_t*>(h_out + base + ncol[f]) = hs[f][tj];
-        *reinterpret_cast<u2_t*>(xn_out + base + ncol[f]) = to_f16x4_native(y);
-      }
+      for (int r = 0; r < 4; ++r) y[r] = (float)hv[r] * inv_rms * (float)gm[r];
+      *res_at(tj, f) = to_f16x4_native(y);
     }
   }
+  __syncthreads();
+  store_rows(xn_out);
 }
 
 }  // namespace
@@ -1045,6 +1099,7 @@ void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* re
   PF_CHECK(a.ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
            "gemm_w4_add_rmsnorm: activations and weights must be 16-byte aligned");
+  PF_CHECK((reinterpret_cast<uintptr_t>(resid) & 15) == 0, "gemm_w4_add_rmsnorm: residual must be 16-byte aligned");
   PF_CHECK(((reinterpret_cast<uintptr_t>(resid) | reinterpret_cast<uintptr_t>(gamma) |
              reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(xn_out) |
              reinterpret_cast<uintptr_t>(a.bias)) & 7) == 0,
@@ -1052,13 +1107,14 @@ void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* re
   PF_CHECK(a.M >= 0 && (long)a.M * a.ldx < (1L << 31), "gemm_w4_add_rmsnorm: activation offsets exceed 32 bits");
   if (a.M == 0) return;
   const int grid = (a.M + RN_BT - 1) / RN_BT;
-  const size_t lds = std::max((size_t)RN_NB * RN_BT * KC * sizeof(uint16_t), (size_t)RN_NW * RN_BT * sizeof(float));
+  static_assert((size_t)RN_NW * RN_BT * sizeof(float) <= (size_t)RN_NB * RN_BT * KC * 2, "row sums fit the buffers");
+  const size_t lds = RN_LDS;
   auto go = [&](auto kern) {
-    static bool attr_set = false;  // per instance
-    if (!attr_set) {
+    static std::map<const void*, bool> attr_set;  // per kernel
+    if (!attr_set[reinterpret_cast<const void*>(kern)]) {
       PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)lds));
-      attr_set = true;
+      attr_set[reinterpret_cast<const void*>(kern)] = true;
     }
     ProfScope ps(b, "gemm_o_add_rmsnorm");
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * RN_NW), lds, b->stream, a, resid, gamma, h_out,
