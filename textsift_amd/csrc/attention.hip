@@ -64,34 +64,66 @@ struct AttnGeom {
 
 // Stages the workgroup's keys kbase .. kbase + ROWS - 1 of kv head g into
 // Ks / Vt (layout of AttnGeom); rows outside [0, T) are zero (their scores
-// are masked).
+// are masked). Every load is issued before any is waited for: K goes HBM ->
+// LDS directly (global_load_lds, 16-byte units; a K row of LDK halves is
+// LDK / 8 units, the last of which is padding and copies the row's first
+// unit), V is loaded into registers and written transposed. Ends with the
+// workgroup barrier.
 template <int HD, int ROWS, int LDK, int LDV, int NT>
 __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float16* Vt, size_t seq0, int g, int kbase,
                                          int tid) {
   static_assert(ROWS % 32 == 0, "V^T staging: whole groups of 8 x 4 keys");
+  static_assert(LDK % 8 == 0 && LDK > HD, "K rows of whole 16-byte units");
   const int T = a.T;
-  for (int i = tid; i < ROWS * (HD / 8); i += NT) {
-    const int r = i / (HD / 8), c = i % (HD / 8);
-    const int key = kbase + r;
-    u4_t kv = {0u, 0u, 0u, 0u};
-    if (key >= 0 && key < T) kv = *reinterpret_cast<const u4_t*>(a.k + (seq0 + key) * a.k_stride + g * HD + c * 8);
-    *reinterpret_cast<u4_t*>(&Ks[r * LDK + c * 8]) = kv;
+  const int wave = tid >> 6;
+  constexpr int UPR = LDK / 8;  // 16-byte units per staged K row
+  constexpr int NK = ROWS * UPR, IK = (NK + NT - 1) / NT;
+#pragma unroll
+  for (int it = 0; it < IK; ++it) {
+    const int u = it * NT + tid;
+    if (u < NK) {
+      const int r = u / UPR, c = u % UPR;
+      const int key = min(max(kbase + r, 0), T - 1);  // rows outside [0, T) are cleared below
+      copy16_to_lds(a.k + (seq0 + key) * a.k_stride + g * HD + (c < HD / 8 ? c : 0) * 8,
+                    (lds_ptr_t)(Ks + (size_t)(it * NT + wave * 64) * 8));
+    }
   }
   // 4 keys x 8 dims per thread; 8 consecutive lanes take 32 consecutive keys
   // of the same 8 dims, so each V^T row write of 16 lanes covers distinct banks
-  for (int i = tid; i < (ROWS / 4) * (HD / 8); i += NT) {
+  constexpr int NV = (ROWS / 4) * (HD / 8), IV = (NV + NT - 1) / NT;
+  u4_t vv[IV][4];
+#pragma unroll
+  for (int it = 0; it < IV; ++it) {
+    const int i = min(it * NT + tid, NV - 1);
     const int c = (i >> 3) % (HD / 8), r4 = ((i & 7) + 8 * ((i >> 3) / (HD / 8))) * 4;
-    h8_t vh[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int key = kbase + r4 + u;
-      u4_t vv = {0u, 0u, 0u, 0u};
-      if (key >= 0 && key < T) vv = *reinterpret_cast<const u4_t*>(a.v + (seq0 + key) * a.v_stride + g * HD + c * 8);
-      vh[u] = __builtin_bit_cast(h8_t, vv);
+      const u4_t v = *reinterpret_cast<const u4_t*>(a.v + (seq0 + min(max(key, 0), T - 1)) * a.v_stride + g * HD + c * 8);
+      vv[it][u] = key >= 0 && key < T ? v : u4_t{0u, 0u, 0u, 0u};
     }
+  }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<h4_t*>(&Vt[(c * 8 + j) * LDV + r4]) = h4_t{vh[0][j], vh[1][j], vh[2][j], vh[3][j]};
+  for (int it = 0; it < IV; ++it) {
+    const int i = it * NT + tid;
+    if (i < NV) {
+      const int c = (i >> 3) % (HD / 8), r4 = ((i & 7) + 8 * ((i >> 3) / (HD / 8))) * 4;
+      h8_t vh[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) vh[u] = __builtin_bit_cast(h8_t, vv[it][u]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<h4_t*>(&Vt[(c * 8 + j) * LDV + r4]) = h4_t{vh[0][j], vh[1][j], vh[2][j], vh[3][j]};
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the K copies
+  __syncthreads();
+  if (kbase < 0 || kbase + ROWS > T) {  // at a sequence end: clear the K rows outside [0, T)
+    for (int u = tid; u < NK; u += NT) {
+      const int key = kbase + u / UPR;
+      if (key < 0 || key >= T) *reinterpret_cast<u4_t*>(Ks + (size_t)u * 8) = u4_t{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
   }
 }
 
@@ -121,7 +153,6 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
   const int kbase = t0 - W;                  // key index of staged row 0
 
   stage_kv<HD, ROWS, LDK, LDV, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
-  __syncthreads();
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
   const int tq = tq0 + l16;                  // this lane's query
@@ -331,7 +362,6 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   const int kbase = t0 - W;                  // key index of staged row 0
 
   stage_kv<HD, ROWS, LDK, LDV, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
-  __syncthreads();
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
   const int tq = tq0 + l16;                  // this lane's query
@@ -352,20 +382,31 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   constexpr float LOG2_E = 1.44269504088896340736f;
   const float sscale = a.scale * LOG2_E;     // scores in the exponent's units
 
-  // this workgroup's query heads: an even split of the group's G heads
-  for (int hh = hgrp * G / a.head_groups; hh < (hgrp + 1) * G / a.head_groups; ++hh) {
+  // this workgroup's query heads: an even split of the group's G heads. The
+  // next head's Q fragments are loaded while this head is processed.
+  const int h_end = (hgrp + 1) * G / a.head_groups;
+  auto load_q = [&](int hq, h8_t (&dst)[NDH]) {
+#pragma unroll
+    for (int dh = 0; dh < NDH; ++dh) {
+      const u4_t v = *reinterpret_cast<const u4_t*>(a.q + (seq0 + min(tq, T - 1)) * a.q_stride + hq * HD + 32 * dh +
+                                                    8 * lg);
+      dst[dh] = __builtin_bit_cast(h8_t, q_ok ? v : u4_t{0u, 0u, 0u, 0u});
+    }
+  };
+  // (raw values: scaled where used, so the load is not waited for at once)
+  auto load_sink = [&](int hq) { return a.sinks ? a.sinks[hq] : -INFINITY; };
+  h8_t qf[NDH];
+  float sink = load_sink(g * G + hgrp * G / a.head_groups);
+  load_q(g * G + hgrp * G / a.head_groups, qf);
+  for (int hh = hgrp * G / a.head_groups; hh < h_end; ++hh) {
     const int hq = g * G + hh;
     // opaque per-head copies of the window bounds (see k_banded_attention)
     int lo = lo0, hi = hi0;
     asm volatile("" : "+v"(lo), "+v"(hi));
-    h8_t qf[NDH];
-#pragma unroll
-    for (int dh = 0; dh < NDH; ++dh) {
-      u4_t v = {0u, 0u, 0u, 0u};
-      if (q_ok) v = *reinterpret_cast<const u4_t*>(a.q + (seq0 + tq) * a.q_stride + hq * HD + 32 * dh + 8 * lg);
-      qf[dh] = __builtin_bit_cast(h8_t, v);
-    }
-    const float sink = a.sinks ? a.sinks[hq] * LOG2_E : -INFINITY;
+    const int hn = hh + 1 < h_end ? hq + 1 : hq;
+    const float sink_n = load_sink(hn);  // issued before the Q loads: waiting for it leaves them in flight
+    h8_t qn[NDH];
+    load_q(hn, qn);
 
     // ---- pass 1: unscaled scores for the whole band, kept in registers;
     // slots outside the query's window and masked keys hold -inf. The K
@@ -424,7 +465,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
     mr = fmaxf(mr, __shfl_xor(mr, 32, 64));
     // max over the scaled scores (scaling by sscale > 0 keeps the order) and the sink;
     // -inf only without a sink and with no valid key (every e is then 0)
-    float m = fmaxf(mr * sscale, sink);
+    const float sink2 = sink * LOG2_E;
+    float m = fmaxf(mr * sscale, sink2);
     m = m == -INFINITY ? 0.0f : m;
     const float nm = -m;
 
@@ -495,7 +537,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         }
       }
     }
-    const float l = lsum[0] + __builtin_amdgcn_exp2f(sink - m);
+    const float l = lsum[0] + __builtin_amdgcn_exp2f(sink2 - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     // lane holds out[tq][hq*HD + 16 dt + 4 lg + r]
     if (q_ok) {
@@ -506,6 +548,9 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         *reinterpret_cast<u2_t*>(orow + 16 * dt + 4 * lg) = to_f16x4_native(ov);
       }
     }
+#pragma unroll
+    for (int dh = 0; dh < NDH; ++dh) qf[dh] = qn[dh];
+    sink = sink_n;
   }
 }
 

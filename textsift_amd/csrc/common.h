@@ -85,6 +85,17 @@ __device__ __forceinline__ float hw_h2f(uint16_t h) {
 
 typedef uint16_t us2_t __attribute__((ext_vector_type(2)));
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i's bytes
+// land at dst + 16 i; dst must be wave-uniform. The builtin exists only for
+// the device pass (clang drops the kernel's host stub if the host pass sees it).
+__device__ __forceinline__ void copy16_to_lds(const void* src, lds_ptr_t dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+#endif
+}
+
 // True when the four fp16 values packed in w are all normal numbers (no
 // zero, subnormal, inf or NaN): wasm_h2f of each is then the hardware
 // widening. Per half h = bits & 0x7fff: 0x0400 <= h < 0x7c00, tested as

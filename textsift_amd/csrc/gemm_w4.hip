@@ -45,17 +45,6 @@ namespace {
 constexpr int KC = 128;  // K per chunk (4 quant blocks, 256 bytes of fp16 activations per row)
 constexpr int NW = 4;    // waves per workgroup, stacked along N
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// 16-byte HBM -> LDS copy per lane (global_load_lds_dwordx4): lane i's bytes
-// land at dst + 16 i; dst must be wave-uniform. The builtin exists only for
-// the device pass (clang drops the kernel's host stub if the host pass sees it).
-__device__ __forceinline__ void copy16_to_lds(const void* src, lds_ptr_t dst) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
-#endif
-}
-
 __device__ __forceinline__ uint32_t h2_bits(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
 // {cos, sin} of pairs pidx and pidx + 1 (pidx even) from row `row` of the
