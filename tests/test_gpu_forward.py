@@ -434,6 +434,42 @@ def test_fused_router_topk_bit_exact(kind):
     assert np.allclose(rw, w_ref, rtol=0.0, atol=2e-7, equal_nan=True)
 
 
+@pytest.mark.parametrize("B,T", [(3, 1000), (9, 2048)], ids=["16-row-router", "64-row-router"])
+def test_router_counts_and_plan(B, T):
+    """Above 1024 rows the router GEMM's top-k epilogue also counts each
+    router tile's rows per expert (16-row tiles up to 16384 rows, 64-row
+    tiles above) and one kernel builds the routing plan from the counts: the
+    counts equal the tapped expert ids' per-tile histogram and the plan is the
+    stable counting sort of those ids (expert.ts:125-145 order)."""
+    E, Vv, K = 128, 512, 4
+    w = synth.make_model_weights(PF_CONFIG, seed=81, num_layers=1, num_experts=E, vocab_size=Vv)
+    be = HipBackend(w, precision=_native.PRECISION_FP16)
+    be.warmup()
+    m = be.model
+    M = B * T
+    m.enable_taps(True)
+    ids = synth.token_ids(82, M, Vv).reshape(B, T)
+    be.forward_batch(ids, np.ones((B, T), np.uint8))
+    idx = m.tap("ridx.0", np.int32, M * K).reshape(M, K)
+    tr = 16 if M <= 16384 else 64
+    n_ct = (M + tr - 1) // tr
+    cnt = m.tap("rcount.0", np.int32, n_ct * E).reshape(n_ct, E)
+    off = m.tap("expert_off.0", np.int32, E + 1)
+    slot_token = m.tap("slot_token.0", np.int32, M * K)
+    slot_of = m.tap("slot_of.0", np.int32, M * K)
+    m.enable_taps(False)
+    be.dispose()
+    for t0 in range(0, M, tr):
+        assert np.array_equal(cnt[t0 // tr], np.bincount(idx[t0:t0 + tr].ravel(), minlength=E)), f"tile {t0 // tr}"
+    flat = idx.ravel()
+    order = np.argsort(flat, kind="stable")
+    assert np.array_equal(slot_token, (order // K).astype(np.int32))
+    inv = np.empty(M * K, np.int64)
+    inv[order] = np.arange(M * K)
+    assert np.array_equal(slot_of, inv)
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]).astype(np.int32))
+
+
 @pytest.mark.parametrize("B,T", [(1, 300), (8, 2048)], ids=["norm-in-router", "fused"])
 def test_o_residual_norm_vs_oracle(small, B, T):
     """The O projection, residual add and RMSNorm (fp16 numerics): below

@@ -462,6 +462,46 @@ def test_moe_route_permutation_bit_exact(be, T, E, tile):
     assert np.array_equal(tiles[:nt, :3], np.array(exp_tiles, np.int32).reshape(-1, 3))
 
 
+@pytest.mark.parametrize("T,E,tile,tile_rows", [(3000, 128, 128, 16), (18432, 128, 128, 64), (2500, 37, 64, 128),
+                                                 (1025, 256, 16, 1024)])
+def test_moe_route_counts_bit_exact(be, T, E, tile, tile_rows):
+    """The one-kernel routing plan from per-tile expert counts (what the
+    router GEMM's top-k epilogue writes) equals the stable counting sort
+    (expert.ts:125-145 order), like the three-kernel path."""
+    K = 4
+    rng = np.random.default_rng(T + E + tile_rows)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    idx = np.stack([rng.choice(E, K, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    S = T * K
+    n_ct = (T + tile_rows - 1) // tile_rows
+    counts = np.zeros((n_ct, E), np.int32)
+    for t0 in range(0, T, tile_rows):
+        counts[t0 // tile_rows] = np.bincount(idx[t0:t0 + tile_rows].ravel(), minlength=E)
+    max_tiles = (S + tile - 1) // tile + E
+    bufs = [be.buffer(idx), be.buffer(counts), be.buffer(nbytes=(E + 1) * 4), be.buffer(nbytes=S * 4),
+            be.buffer(nbytes=S * 4), be.buffer(nbytes=max_tiles * 16), be.buffer(nbytes=4)]
+    be.dispatch("moe_route_counts", bufs, u32s(T, K, E, tile, tile_rows))
+    off = bufs[2].read(np.int32)
+    slot_token = bufs[3].read(np.int32)
+    slot_of = bufs[4].read(np.int32).reshape(T, K)
+    tiles = bufs[5].read(np.int32).reshape(-1, 4)
+    nt = int(bufs[6].read(np.int32)[0])
+    for b in bufs:
+        b.release()
+    flat = idx.ravel()
+    order = np.argsort(flat, kind="stable")
+    assert np.array_equal(slot_token, (order // K).astype(np.int32))
+    inv = np.empty(S, np.int64)
+    inv[order] = np.arange(S)
+    assert np.array_equal(slot_of.ravel(), inv)
+    cnt = np.bincount(flat, minlength=E)
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32))
+    exp_tiles = [(e, off[e] + r, min(tile, cnt[e] - r)) for e in range(E) for r in range(0, cnt[e], tile)]
+    assert nt == len(exp_tiles)
+    assert np.array_equal(tiles[:nt, :3], np.array(exp_tiles, np.int32).reshape(-1, 3))
+
+
 # ---------------------------------------------------------------- MoE layer (config 3)
 
 def zipf_router(T, D, E, seed):

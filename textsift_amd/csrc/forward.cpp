@@ -383,6 +383,13 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   // holds whole 640-wide rows) or as its own kernel
   const bool fused_o = f16 && D == 640 && (Hq * hd == 640 || Hq * hd == 896) && M >= 16384;
   const bool norm_in_router = f16 && !fused_o && D == 640 && small_dense(D, 8 * SMALL_M);
+  // fp16 numerics with the model's 128 experts and top-4: the router GEMM's
+  // epilogue selects the experts (bit-identical to router_topk) and, above
+  // one counting block of tokens, counts each router tile's rows per expert,
+  // from which one kernel builds the routing plan
+  const bool fused_topk = f16 && E == 128 && K == 4;
+  const int router_tile = small_dense(D, 8 * SMALL_M) ? 16 : 64;
+  const bool route_counts = fused_topk && M > 1024;
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
@@ -453,16 +460,13 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
       }
       a.w = L.router.q; a.ws = L.router.s; a.wz = L.router.z; a.bias = L.router.bias;
       a.out = s.rlogits; a.ldo = E; a.M = M; a.N = E; a.K = D;
-      // fp16 numerics with the model's 128 experts and top-4: the router
-      // GEMM's epilogue selects the experts (bit-identical to router_topk)
-      const bool fused_topk = f16 && E == 128 && K == 4;
       if (f16) {
         a.w = reinterpret_cast<const uint8_t*>(L.router4.w); a.wsz = L.router4.sz;
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
+          if (route_counts) a.topk_counts = plan.tile_counts;  // per router tile: the routing plan's counts
         }
-        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, small_dense(D, 8 * SMALL_M) ? 16 : 64, 2,
-                "gemm_router");
+        gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, router_tile, 2, "gemm_router");
       } else {
         gemm_int4(b, a, XKind::SPLIT, Epi::F32, false, 128, "gemm_router");
       }
@@ -473,7 +477,15 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     record_tap(m, "router." + tag, s.rlogits, (size_t)M * E * 4);
     record_tap(m, "ridx." + tag, s.ridx, (size_t)M * K * 4);
     record_tap(m, "rw." + tag, s.rw, (size_t)M * K * 4);
-    moe_route(b, s.ridx, M, K, E, plan);
+    if (route_counts) {
+      record_tap(m, "rcount." + tag, plan.tile_counts, (size_t)((M + router_tile - 1) / router_tile) * E * 4);
+      moe_route_counts(b, s.ridx, plan.tile_counts, router_tile, M, K, E, plan);
+    } else {
+      moe_route(b, s.ridx, M, K, E, plan);
+    }
+    record_tap(m, "expert_off." + tag, plan.expert_off, (size_t)(E + 1) * 4);
+    record_tap(m, "slot_token." + tag, plan.slot_token, (size_t)M * K * 4);
+    record_tap(m, "slot_of." + tag, plan.slot_of, (size_t)M * K * 4);
     {
       GemmArgs g;
       g.x = s.xn_hi; g.x_lo = s.xn_lo; g.ldx = D; g.row_map = plan.slot_token;

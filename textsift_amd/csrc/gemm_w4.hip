@@ -116,11 +116,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int PLANE = BT * KC;    // halves per plane per buffer
 
   extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [2][XS][BT][KC] swizzled
+  // top-k epilogue: the tile's rows per expert (cleared here; barriers follow before use)
+  __shared__ int topk_hist[EPI == Epi::F32_TOPK ? 128 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
+  if constexpr (EPI == Epi::F32_TOPK)
+    if (p.topk_counts && tid < 128) topk_hist[tid] = 0;
 
   const int n_tiles = (p.N + BN - 1) / BN;
   // Grouped: the grid covers the largest possible tile list; only the first
@@ -578,6 +582,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         if (nan) topk_insertion<4>(at, 128, V, I);
         const size_t t = (size_t)(row0 + row);
         topk_write<4>(V, I, p.topk_wscale, p.topk_idx + t * 4, p.topk_w + t * 4);
+        if (p.topk_counts) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) atomicAdd(&topk_hist[I[k]], 1);  // order-free: the counts are exact
+        }
+      }
+      if (p.topk_counts) {
+        __syncthreads();
+        if (tid < 128) p.topk_counts[(size_t)(row0 / BT) * 128 + tid] = topk_hist[tid];
       }
     }
     return;

@@ -617,6 +617,114 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
   }
 }
 
+// The same plan from per-tile expert counts, in one kernel instead of count,
+// scan and scatter: counts[tile][e] holds the tokens of tile `tile` (tiles of
+// RBLK / ct_per_blk rows) routed to expert e (the router GEMM's top-k
+// epilogue writes them). Block blk sums, per expert, the counts of every tile
+// (the expert's total) and of the tiles before its first token (its base
+// within the expert), scans the totals over experts, and assigns its tokens'
+// slots by bitmap ranks as k_moe_scatter does. Block 0 also writes
+// expert_off, the tile list and num_tiles. Same outputs as the three kernels.
+__global__ __launch_bounds__(RBLK) void k_moe_route_counts(const int32_t* __restrict__ idx,
+                                                           const int32_t* __restrict__ counts, int n_ct,
+                                                           int ct_per_blk, int32_t* __restrict__ expert_off,
+                                                           int32_t* __restrict__ slot_token,
+                                                           int32_t* __restrict__ slot_of, int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ num_tiles, int T, int K, int E,
+                                                           int tile_t) {
+  __shared__ uint32_t bits[256 * BWS];
+  __shared__ int32_t psum[2][RBLK];  // per (quarter of the tiles, expert): all tiles, tiles before the block
+  __shared__ int32_t off[256], ebase[256], toff[256], wsum[2][RBLK / 64];
+  __shared__ uint16_t pre[256 * BWS];
+  const int blk = blockIdx.x, t0 = blk * RBLK, ntok = min(RBLK, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  {
+    const int e = tid & 255, q = tid >> 8;  // a quarter of the tiles per thread
+    const int tb = blk * ct_per_blk;
+    const int per = (n_ct + 3) / 4, lo = min(n_ct, q * per), hi = min(n_ct, lo + per);
+    int sa = 0, sb = 0;
+    if (e < E) {
+      int t = lo;
+      for (; t + 8 <= hi; t += 8) {  // independent loads in flight
+        int c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] = counts[(size_t)(t + u) * E + e];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          sa += c[u];
+          sb += t + u < tb ? c[u] : 0;
+        }
+      }
+      for (; t < hi; ++t) {
+        const int c = counts[(size_t)t * E + e];
+        sa += c;
+        sb += t < tb ? c : 0;
+      }
+    }
+    psum[0][tid] = sa;
+    psum[1][tid] = sb;
+  }
+  moe_block_bitmap(idx, bits, t0, ntok, K, E);  // (its barriers also publish psum)
+  // rows c and tiles n of expert e = tid; inclusive scans within the wave
+  int c = 0, below = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c += psum[0][q * 256 + tid];
+      below += psum[1][q * 256 + tid];
+    }
+  }
+  const int n = (c + tile_t - 1) / tile_t;
+  int ci = c, ni = n;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(ci, o, 64), bb = __shfl_up(ni, o, 64);
+    if (lane >= o) {
+      ci += a;
+      ni += bb;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][wv] = ci;
+    wsum[1][wv] = ni;
+  }
+  __syncthreads();
+  int cb = 0, nbase = 0, ct = 0, nt = 0;
+#pragma unroll
+  for (int w = 0; w < RBLK / 64; ++w) {
+    cb += w < wv ? wsum[0][w] : 0;
+    nbase += w < wv ? wsum[1][w] : 0;
+    ct += wsum[0][w];
+    nt += wsum[1][w];
+  }
+  const int base = cb + ci - c;  // exclusive prefix of rows
+  if (tid < E) {
+    ebase[tid] = base;
+    off[tid] = base + below;
+    toff[tid] = nbase + ni - n;  // exclusive prefix of tiles
+    if (blk == 0) expert_off[tid] = base;
+  }
+  if (blk == 0 && tid == 0) {
+    expert_off[E] = ct;
+    *num_tiles = nt;
+  }
+  __syncthreads();
+  if (blk == 0) moe_write_tiles(toff, ebase, ct, E, nt, tile_t, tiles);
+  moe_word_prefix(bits, pre, E);
+  if (tid >= ntok) return;
+  const int wl = tid >> 5;
+  const uint32_t lower = (1u << (tid & 31)) - 1u;
+  for (int k = 0; k < K; ++k) {
+    const size_t i = (size_t)(t0 + tid) * K + k;
+    const int e = idx[i];
+    if ((unsigned)e >= (unsigned)E) continue;
+    const int rank = pre[e * BWS + wl] + __popc(bits[e * BWS + wl] & lower);
+    const int pos = off[e] + rank;
+    slot_token[pos] = t0 + tid;
+    slot_of[i] = pos;
+  }
+}
+
 // ----------------------------------------------------------------------------
 // MoE combine (scatter_add_weighted_f32 :1027-1055 + cast_f32_to_fp16_scaled
 // :1153-1164 + add_fp16). Each token sums its K expert outputs in ascending
@@ -1186,7 +1294,7 @@ static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t moe_plan_bytes(int T, int K, int E, int tile_t) {
   const size_t nblk = (size_t)(T + RBLK - 1) / RBLK;
   return al256(nblk * E * 4) * 2 + al256((size_t)(E + 1) * 4) + al256((size_t)T * K * 4) * 2 +
-         al256((size_t)moe_max_tiles(T, K, E, tile_t) * 16) + 256;
+         al256((size_t)moe_max_tiles(T, K, E, tile_t) * 16) + 256 + al256((size_t)(T + 15) / 16 * E * 4);
 }
 
 MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t) {
@@ -1199,7 +1307,8 @@ MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t) {
   m.slot_token = reinterpret_cast<int32_t*>(p); p += al256((size_t)T * K * 4);
   m.slot_of = reinterpret_cast<int32_t*>(p); p += al256((size_t)T * K * 4);
   m.tiles = reinterpret_cast<int32_t*>(p); p += al256((size_t)moe_max_tiles(T, K, E, tile_t) * 16);
-  m.num_tiles = reinterpret_cast<int32_t*>(p);
+  m.num_tiles = reinterpret_cast<int32_t*>(p); p += 256;
+  m.tile_counts = reinterpret_cast<int32_t*>(p);
   m.max_tiles = moe_max_tiles(T, K, E, tile_t);
   m.tile_t = tile_t;
   return m;
@@ -1235,6 +1344,19 @@ void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const 
                        T, K, E);
     PF_HIP(hipGetLastError());
   }
+}
+
+void moe_route_counts(pfhip_backend* b, const int32_t* idx, const int32_t* counts, int tile_rows, int T, int K, int E,
+                      const MoePlan& m) {
+  PF_CHECK(E >= 1 && E <= 256 && K >= 1 && K <= MAXK, "moe_route_counts: need E <= 256 and K <= 8");
+  PF_CHECK(tile_rows >= 1 && RBLK % tile_rows == 0, "moe_route_counts: the count tiles must divide 1024 rows");
+  PF_CHECK(counts, "moe_route_counts: null counts");
+  if (T <= 0) return;
+  const int nblk = (T + RBLK - 1) / RBLK, n_ct = (T + tile_rows - 1) / tile_rows;
+  ProfScope ps(b, "moe_route");
+  hipLaunchKernelGGL(k_moe_route_counts, dim3(nblk), dim3(RBLK), 0, b->stream, idx, counts, n_ct, RBLK / tile_rows,
+                     m.expert_off, m.slot_token, m.slot_of, m.tiles, m.num_tiles, T, K, E, m.tile_t);
+  PF_HIP(hipGetLastError());
 }
 
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,

@@ -123,6 +123,8 @@ struct GemmArgs {
   float* topk_w = nullptr;
   int topk_k = 0;
   float topk_wscale = 1.0f;
+  // F32_TOPK: when set, [M / BT][128] counts of each tile's rows routed to each expert
+  int32_t* topk_counts = nullptr;
   // Residual add + RMSNorm on the way in (gemm_w4, 16-token tile, K == 640):
   // x is the fp16 O projection output o; the kernel forms h2 = fp16(o + res)
   // and xn = fp16(h2 * inv_rms(o + res) * gamma), writes both, and multiplies xn.
@@ -203,6 +205,7 @@ struct MoePlan {
   int32_t* slot_of;     // [T*K]  slot of (token, k)
   int32_t* tiles;       // [max_tiles][4]
   int32_t* num_tiles;   // [1]
+  int32_t* tile_counts; // [ceil(T / 16)][E] expert counts per router tile (moe_route_counts)
   int max_tiles;
   int tile_t;
 };
@@ -210,6 +213,11 @@ int moe_max_tiles(int T, int K, int E, int tile_t);
 size_t moe_plan_bytes(int T, int K, int E, int tile_t);
 MoePlan moe_plan_carve(void* base, int T, int K, int E, int tile_t);
 void moe_route(pfhip_backend* b, const int32_t* idx, int T, int K, int E, const MoePlan& plan);
+// The same plan from counts[tile][e] of the tokens' tiles of tile_rows rows
+// (tile_rows divides 1024; written by the router GEMM's top-k epilogue):
+// one kernel instead of three.
+void moe_route_counts(pfhip_backend* b, const int32_t* idx, const int32_t* counts, int tile_rows, int T, int K, int E,
+                      const MoePlan& plan);
 // y: the expert outputs in slot order, fp16 when y16 (the fp16 numerics), else f32;
 // residual NULL: no residual (the outputs hold the MoE result alone).
 void moe_combine(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,

@@ -525,6 +525,29 @@ static std::vector<KernelEntry>& registry() {
                  m.num_tiles = bp<int32_t>(bs, 5);
                  moe_route(b, bp<int32_t>(bs, 0), T, K, E, m);
                }});
+  // moe_route_counts: the same plan from counts[tile][e] of tiles of tile_rows rows.
+  // push {T, K, E, tile_t, tile_rows}; bindings [routing_idx, counts, expert_off, slot_token, slot_of, tiles,
+  // num_tiles]
+  r.push_back({"moe_route_counts", 7, 20, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int T = (int)pu(p, 0), K = (int)pu(p, 1), E = (int)pu(p, 2), tt = (int)pu(p, 3);
+                 const int tr = (int)pu(p, 4);
+                 PF_CHECK(tt == 16 || tt == 64 || tt == 128, "moe_route_counts: tile_t must be 16, 64 or 128");
+                 PF_CHECK(tr >= 1 && 1024 % tr == 0, "moe_route_counts: tile_rows must divide 1024");
+                 need(bs, 0, (size_t)T * K * 4, "moe_route_counts");
+                 need(bs, 1, (size_t)((T + tr - 1) / tr) * E * 4, "moe_route_counts");
+                 need(bs, 2, (size_t)(E + 1) * 4, "moe_route_counts");
+                 need(bs, 3, (size_t)T * K * 4, "moe_route_counts");
+                 need(bs, 4, (size_t)T * K * 4, "moe_route_counts");
+                 need(bs, 5, (size_t)moe_max_tiles(T, K, E, tt) * 16, "moe_route_counts");
+                 need(bs, 6, 4, "moe_route_counts");
+                 MoePlan m = moe_plan_carve(backend_scratch(b, moe_plan_bytes(T, K, E, tt)), T, K, E, tt);
+                 m.expert_off = bp<int32_t>(bs, 2);
+                 m.slot_token = bp<int32_t>(bs, 3);
+                 m.slot_of = bp<int32_t>(bs, 4);
+                 m.tiles = bp<int32_t>(bs, 5);
+                 m.num_tiles = bp<int32_t>(bs, 6);
+                 moe_route_counts(b, bp<int32_t>(bs, 0), bp<int32_t>(bs, 1), tr, T, K, E, m);
+               }});
   // moe_ffn: one MoE FFN layer.
   // push {T, D, E, K, dff, router_int4 (0: fp16 router W [D][E]; 1: MatMulNBits router), x_f32, precision}
   // precision 0: the split numerics (gemm_int4, f32 activations as hi/lo planes, per-block f32 scaling);
