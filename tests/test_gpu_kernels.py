@@ -298,6 +298,24 @@ def test_norms_vs_oracle(be):
     assert rel_err_max(out.view(np.float32), nref.ravel()) < 1e-6
 
 
+def test_rms_norm_zeros_and_subnormals(be):
+    """Exact zeros (common in the embedding's output) take the hardware
+    widening, subnormals the reference's blind rebias (zig/math.zig:45-52):
+    8195 rows against the oracle, and the first 333 bit-identical to a
+    333-row call."""
+    T, D = 8195, 640
+    x = synth.to_fp16_bits(synth.normal(410, T * D, 0, 2))
+    x[::7] = 0
+    x[3::101] = (np.arange(x[3::101].size) % 0x3ff + 1).astype(np.uint16) | 0x8000 * (np.arange(x[3::101].size) & 1)
+    x = x.reshape(T, D)
+    g = synth.to_fp16_bits(synth.normal(411, D, 1, 0.1))
+    out = run(be, "rms_norm", [x, g], T * D * 2, push(T, D, 1e-5, 0)).view(np.uint16).reshape(T, D)
+    head = run(be, "rms_norm", [x[:333], g], 333 * D * 2, push(333, D, 1e-5, 0)).view(np.uint16).reshape(333, D)
+    assert np.array_equal(out[:333], head)
+    ref = oracle.rms_norm(x, g, T, D, 1e-5)
+    assert fp16_ulp_diff(out, ref).max() <= 1.0 and np.mean(out == ref) > 0.999
+
+
 def test_elementwise_fixtures(be, fixture):
     fx = fixture("add_fp16")
     out = run(be, "add_fp16", [fx.input("a", np.uint16), fx.input("b", np.uint16)], 512,

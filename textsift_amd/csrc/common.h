@@ -96,16 +96,17 @@ __device__ __forceinline__ void copy16_to_lds(const void* src, lds_ptr_t dst) {
 #endif
 }
 
-// True when the four fp16 values packed in w are all normal numbers (no
-// zero, subnormal, inf or NaN): wasm_h2f of each is then the hardware
-// widening. Per half h = bits & 0x7fff: 0x0400 <= h < 0x7c00, tested as
-// (h - 0x0400) mod 2^16 < 0x7800 with packed 16-bit arithmetic.
+// True when wasm_h2f of each of the four fp16 values packed in w is the
+// hardware widening: every value is zero or normal (no subnormal, inf or
+// NaN). Per half h = bits & 0x7fff, with packed 16-bit arithmetic:
+// (h - 1) mod 2^16 >= 0x3ff excludes the subnormals (zero wraps to 0xffff)
+// and h < 0x7c00 excludes inf and NaN.
 __device__ __forceinline__ bool h4_normal(u2_t w) {
-  const us2_t k = {0x0400, 0x0400};
-  const us2_t a = __builtin_bit_cast(us2_t, w.x & 0x7fff7fffu) - k;
-  const us2_t b = __builtin_bit_cast(us2_t, w.y & 0x7fff7fffu) - k;
-  const us2_t m = __builtin_elementwise_max(a, b);
-  return (m.x < 0x7800) & (m.y < 0x7800);
+  const us2_t one = {1, 1};
+  const us2_t hx = __builtin_bit_cast(us2_t, w.x & 0x7fff7fffu), hy = __builtin_bit_cast(us2_t, w.y & 0x7fff7fffu);
+  const us2_t lo = __builtin_elementwise_min(hx - one, hy - one);
+  const us2_t hi = __builtin_elementwise_max(hx, hy);
+  return (lo.x >= 0x3ff) & (lo.y >= 0x3ff) & (hi.x < 0x7c00) & (hi.y < 0x7c00);
 }
 
 __device__ __noinline__ f4_t h4_widen_exact(u2_t w) {
@@ -114,7 +115,7 @@ __device__ __noinline__ f4_t h4_widen_exact(u2_t w) {
 }
 
 // wasm_h2f of four packed fp16 values: the hardware widening when all are
-// normal, the exact software path (not inlined) otherwise.
+// zero or normal, the exact software path (not inlined) otherwise.
 __device__ __forceinline__ void h4_widen(u2_t w, float v[4]) {
   if (h4_normal(w)) {
     v[0] = hw_h2f((uint16_t)(w.x & 0xFFFFu));
