@@ -6,9 +6,12 @@ ROCm toolchain) and scanned for instruction forms the kernels must not use:
     build disables the feature;
   * scalar memory writes (s_store*, s_buffer_store*, s_atomic*,
     s_dcache_wb*): every store is a vector store;
-  * fused mixed-precision conversions (v_fma_mix*): they round a product once
-    to fp16 where the reference rounds to f32 first. They are allowed only in
-    the RoPE epilogue instances, whose products (fp16 x fp16) are exact in f32.
+  * fused mixed-precision conversions to fp16 (v_fma_mixlo_f16,
+    v_fma_mixhi_f16): they round a product once to fp16 where the reference
+    rounds to f32 first. They are allowed only in the RoPE epilogue
+    instances, whose products (fp16 x fp16) are exact in f32. v_fma_mix_f32
+    (an f32 result) widens its fp16 operands exactly and rounds once to f32:
+    it is the f32 fma of the widened values and is allowed anywhere.
 """
 import os
 import re
@@ -91,6 +94,6 @@ def test_no_scalar_memory_writes(device_code):
 
 
 def test_fused_mixed_conversions_only_in_rope(device_code):
-    bad = {f for f, ins in device_code.items() if any(i.startswith("v_fma_mix") for i in ins)
+    bad = {f for f, ins in device_code.items() if any(i.startswith(("v_fma_mixlo", "v_fma_mixhi")) for i in ins)
            and "Epi)2" not in f and "EpiE2" not in f}
     assert not bad, sorted(bad)
