@@ -79,6 +79,14 @@ size_t z_bytes(size_t N, size_t K) { return N * ((K / 32 + 1) / 2); }
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Copies on the backend's stream, waited for: the stream is non-blocking, so
+// copies on the null stream would not be ordered before its kernels (a
+// pageable host -> device hipMemcpy may return before its DMA has landed).
+void copy_sync(pfhip_backend* b, void* dst, const void* src, size_t n, hipMemcpyKind kind) {
+  PF_HIP(hipMemcpyAsync(dst, src, n, kind, b->stream));
+  PF_HIP(hipStreamSynchronize(b->stream));
+}
+
 }  // namespace
 
 struct pfhip_model {
@@ -323,9 +331,9 @@ static void ensure_rope(pfhip_model* m, int T) {
   PF_HIP(hipMalloc(&m->rope_cos, csf.size() * 4));
   PF_HIP(hipMalloc(&m->rope_sin, snf.size() * 4));
   PF_HIP(hipMalloc(&m->rope_pairs, pairs.size() * 2));
-  PF_HIP(hipMemcpy(m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice));
-  PF_HIP(hipMemcpy(m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice));
-  PF_HIP(hipMemcpy(m->rope_pairs, pairs.data(), pairs.size() * 2, hipMemcpyHostToDevice));
+  copy_sync(b, m->rope_cos, csf.data(), csf.size() * 4, hipMemcpyHostToDevice);
+  copy_sync(b, m->rope_sin, snf.data(), snf.size() * 4, hipMemcpyHostToDevice);
+  copy_sync(b, m->rope_pairs, pairs.data(), pairs.size() * 2, hipMemcpyHostToDevice);
   m->rope_T = T;
 }
 
@@ -613,12 +621,13 @@ int pfhip_model_set_weight(pfhip_model* m, const char* name, const void* bytes, 
                  std::to_string(it->second));
     auto& t = m->w[name];
     if (t.p && t.n < n) {
+      PF_HIP(hipStreamSynchronize(m->b->stream));
       hipFree(t.p);
       t.p = nullptr;
     }
     if (!t.p) PF_HIP(hipMalloc(&t.p, al256(n)));
     t.n = n;
-    PF_HIP(hipMemcpy(t.p, bytes, n, hipMemcpyHostToDevice));
+    copy_sync(m->b, t.p, bytes, n, hipMemcpyHostToDevice);
     m->finalized = false;
     return 0;
   } catch (const std::exception& ex) {
@@ -654,13 +663,13 @@ int pfhip_model_finalize(pfhip_model* m, char* err, size_t cap) {
       for (auto& nm : {std::make_pair("q_proj", Nq), std::make_pair("k_proj", Nk), std::make_pair("v_proj", Nk)}) {
         const std::string wp = p + "attn." + nm.first;
         const size_t n = nm.second;
-        PF_HIP(hipMemcpy((char*)fq.p + q_bytes(row, D), W<uint8_t>(m, wp + ".int4"), q_bytes(n, D),
-                         hipMemcpyDeviceToDevice));
-        PF_HIP(hipMemcpy((char*)fs.p + s_bytes(row, D), W<uint16_t>(m, wp + ".scales"), s_bytes(n, D),
-                         hipMemcpyDeviceToDevice));
-        PF_HIP(hipMemcpy((char*)fz.p + z_bytes(row, D), W<uint8_t>(m, wp + ".zp"), z_bytes(n, D),
-                         hipMemcpyDeviceToDevice));
-        PF_HIP(hipMemcpy((char*)fb.p + row * 2, W<uint16_t>(m, wp + ".bias"), n * 2, hipMemcpyDeviceToDevice));
+        copy_sync(m->b, (char*)fq.p + q_bytes(row, D), W<uint8_t>(m, wp + ".int4"), q_bytes(n, D),
+                  hipMemcpyDeviceToDevice);
+        copy_sync(m->b, (char*)fs.p + s_bytes(row, D), W<uint16_t>(m, wp + ".scales"), s_bytes(n, D),
+                  hipMemcpyDeviceToDevice);
+        copy_sync(m->b, (char*)fz.p + z_bytes(row, D), W<uint8_t>(m, wp + ".zp"), z_bytes(n, D),
+                  hipMemcpyDeviceToDevice);
+        copy_sync(m->b, (char*)fb.p + row * 2, W<uint16_t>(m, wp + ".bias"), n * 2, hipMemcpyDeviceToDevice);
         row += n;
       }
       m->owned.push_back(fq);
