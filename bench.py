@@ -58,6 +58,7 @@ KERNEL_LABELS = [
     ("add_rmsnorm_f16", ("k_add_rms_norm",)),
     ("router_topk", ("k_router_topk",)),
     ("moe_route", ("k_moe_route_small",)),
+    ("moe_route", ("k_moe_route_counts",)),
     ("moe_count", ("k_moe_count",)),
     ("moe_scan", ("k_moe_scan",)),
     ("moe_scatter", ("k_moe_scatter",)),
