@@ -63,13 +63,14 @@ struct AttnGeom {
 };
 
 // Stages the workgroup's keys kbase .. kbase + ROWS - 1 of kv head g into
-// Ks / Vt (layout of AttnGeom); rows outside [0, T) are zero (their scores
-// are masked). Every load is issued before any is waited for: K goes HBM ->
+// Ks / Vt (layout of AttnGeom); V rows outside [0, T) are zero, K rows
+// outside [0, T) are zero with ZERO_K and otherwise not written (their
+// scores are masked before any use). Every load is issued before any is waited for: K goes HBM ->
 // LDS directly (global_load_lds, 16-byte units; a K row of LDK halves is
 // LDK / 8 units, the last of which is padding and copies the row's first
 // unit), V is loaded into registers and written transposed. Ends with the
 // workgroup barrier.
-template <int HD, int ROWS, int LDK, int LDV, int NT>
+template <int HD, int ROWS, int LDK, int LDV, int NT, bool ZERO_K = true>
 __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float16* Vt, size_t seq0, int g, int kbase,
                                          int tid) {
   static_assert(ROWS % 32 == 0, "V^T staging: whole groups of 8 x 4 keys");
@@ -81,12 +82,11 @@ __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float
 #pragma unroll
   for (int it = 0; it < IK; ++it) {
     const int u = it * NT + tid;
-    if (u < NK) {
-      const int r = u / UPR, c = u % UPR;
-      const int key = min(max(kbase + r, 0), T - 1);  // rows outside [0, T) are cleared below
+    const int r = u / UPR, c = u % UPR;
+    const int key = kbase + r;
+    if (u < NK && key >= 0 && key < T)  // rows outside [0, T) are cleared below
       copy16_to_lds(a.k + (seq0 + key) * a.k_stride + g * HD + (c < HD / 8 ? c : 0) * 8,
                     (lds_ptr_t)(Ks + (size_t)(it * NT + wave * 64) * 8));
-    }
   }
   // 4 keys x 8 dims per thread; 8 consecutive lanes take 32 consecutive keys
   // of the same 8 dims, so each V^T row write of 16 lanes covers distinct banks
@@ -118,7 +118,7 @@ __device__ __forceinline__ void stage_kv(const AttnArgs& a, _Float16* Ks, _Float
   }
   __builtin_amdgcn_s_waitcnt(0);  // the K copies
   __syncthreads();
-  if (kbase < 0 || kbase + ROWS > T) {  // at a sequence end: clear the K rows outside [0, T)
+  if (ZERO_K && (kbase < 0 || kbase + ROWS > T)) {  // at a sequence end: clear the K rows outside [0, T)
     for (int u = tid; u < NK; u += NT) {
       const int key = kbase + u / UPR;
       if (key < 0 || key >= T) *reinterpret_cast<u4_t*>(Ks + (size_t)u * 8) = u4_t{0u, 0u, 0u, 0u};
@@ -361,7 +361,9 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
   const size_t seq0 = (size_t)bseq * T;
   const int kbase = t0 - W;                  // key index of staged row 0
 
-  stage_kv<HD, ROWS, LDK, LDV, 64 * NW>(a, Ks, Vt, seq0, g, kbase, tid);
+  // (K rows outside the sequence stay unwritten: every score of one is
+  // replaced by -inf before the maximum and the exponentials)
+  stage_kv<HD, ROWS, LDK, LDV, 64 * NW, false>(a, Ks, Vt, seq0, g, kbase, tid);
 
   const int tq0 = t0 + 16 * wave;            // this wave's first query
   const int tq = tq0 + l16;                  // this lane's query

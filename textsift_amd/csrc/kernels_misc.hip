@@ -840,126 +840,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
   }
 }
 
-// The same combine for fp16 expert outputs, K = 4 and D = 128 UPL: four
-// tokens per wave, 16 lanes per token, each lane taking the row's 16-byte
-// units q, q + 16, ... (q = lane % 16), so every load and store is a whole
-// 16-byte unit and a wave keeps 4 x 5 rows of units in flight. Per element
-// the arithmetic is k_moe_combine's; the row's sum of squares is taken per
-// lane over its units in order, then over the token's 16 lanes.
-template <int NMODE, bool RES, int UPL>
-__global__ __launch_bounds__(256) void k_moe_combine16(const int32_t* __restrict__ idx, const float* __restrict__ w,
-                                                       const int32_t* __restrict__ slot_of,
-                                                       const uint16_t* __restrict__ y,
-                                                       const uint16_t* __restrict__ residual,
-                                                       uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
-                                                       const uint16_t* __restrict__ gamma,
-                                                       uint16_t* __restrict__ norm_hi, uint16_t* __restrict__ norm_lo,
-                                                       int T, float eps) {
-  constexpr int K = 4, D = 128 * UPL;
-  const int lane = threadIdx.x & 63, q = lane & 15;
-  const int t = (blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6)) * 4 + (lane >> 4);
-  const int tc = min(t, T - 1);  // lanes past T compute the last token again (never stored)
-  int ek[K], sk[K];
-  float wk[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    ek[k] = idx[(size_t)tc * K + k];
-    wk[k] = w[(size_t)tc * K + k];
-    sk[k] = slot_of[(size_t)tc * K + k];
-  }
-#pragma unroll
-  for (int a = 1; a < K; ++a)
-#pragma unroll
-    for (int j = a; j > 0; --j) {
-      const bool sw = ek[j] < ek[j - 1];
-      const int e0 = ek[j - 1], e1 = ek[j], s0 = sk[j - 1], s1 = sk[j];
-      const float w0 = wk[j - 1], w1 = wk[j];
-      ek[j - 1] = sw ? e1 : e0;
-      ek[j] = sw ? e0 : e1;
-      sk[j - 1] = sw ? s1 : s0;
-      sk[j] = sw ? s0 : s1;
-      wk[j - 1] = sw ? w1 : w0;
-      wk[j] = sw ? w0 : w1;
-    }
-  const size_t base = (size_t)tc * D;
-  u4_t yv[UPL][K], rw[UPL], gw[UPL];
-#pragma unroll
-  for (int u = 0; u < UPL; ++u) {
-    const int d = (q + 16 * u) * 8;
-#pragma unroll
-    for (int k = 0; k < K; ++k) yv[u][k] = *reinterpret_cast<const u4_t*>(y + (size_t)sk[k] * D + d);
-    rw[u] = RES ? *reinterpret_cast<const u4_t*>(residual + base + d) : u4_t{0u, 0u, 0u, 0u};
-    if constexpr (NMODE >= 0) gw[u] = *reinterpret_cast<const u4_t*>(gamma + d);
-  }
-  const bool store = t < T;
-  u4_t hs[UPL];
-  float ss = 0.0f;
-#pragma unroll
-  for (int u = 0; u < UPL; ++u) {
-    const int d = (q + 16 * u) * 8;
-    u2_t mo[2], ho[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const h4_t h = __builtin_bit_cast(h4_t, u2_t{yv[u][k][2 * hf], yv[u][k][2 * hf + 1]});
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], (float)h[r], acc[r]);
-      }
-      mo[hf] = to_f16x4(acc);
-      float mv[4], rv[4], sv[4];
-      h4_to_f(mo[hf], mv);
-      h4_to_f(u2_t{rw[u][2 * hf], rw[u][2 * hf + 1]}, rv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sv[r] = rv[r] + mv[r];
-      ho[hf] = to_f16x4(sv);
-      float hv[4];
-      h4_to_f(ho[hf], hv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ss += hv[r] * hv[r];
-    }
-    hs[u] = u4_t{ho[0].x, ho[0].y, ho[1].x, ho[1].y};
-    if (store) {
-      if (moe_out) *reinterpret_cast<u4_t*>(moe_out + base + d) = u4_t{mo[0].x, mo[0].y, mo[1].x, mo[1].y};
-      *reinterpret_cast<u4_t*>(h_out + base + d) = hs[u];
-    }
-  }
-  if constexpr (NMODE >= 0) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);  // the token's 16 lanes
-    const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
-    if (store) {
-#pragma unroll
-      for (int u = 0; u < UPL; ++u) {
-        const int d = (q + 16 * u) * 8;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          float hv[4], gm[4], yo[4];
-          h4_to_f(u2_t{hs[u][2 * hf], hs[u][2 * hf + 1]}, hv);
-          h4_to_f(u2_t{gw[u][2 * hf], gw[u][2 * hf + 1]}, gm);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) yo[r] = hv[r] * inv_rms * gm[r];
-          put4<NMODE>(norm_hi, norm_lo, base + d + 4 * hf, yo);
-        }
-      }
-    }
-  }
-}
-
 template <int NMODE, bool Y16, bool RES>
 void launch_combine_t(pfhip_backend* b, const int32_t* idx, const float* w, const int32_t* slot_of, const void* y,
                       const uint16_t* residual, uint16_t* moe_out, uint16_t* h_out, const uint16_t* gamma,
                       uint16_t* norm_hi, uint16_t* norm_lo, int T, int K, int D, float eps) {
-  if constexpr (Y16) {
-    if (K == 4 && D == 640) {  // the model's shape: whole 16-byte units, 4 tokens per wave
-      const dim3 g16((T + 4 * ROWS_PER_BLOCK - 1) / (4 * ROWS_PER_BLOCK));
-      hipLaunchKernelGGL((k_moe_combine16<NMODE, RES, 5>), g16, dim3(256), 0, b->stream, idx, w, slot_of,
-                         static_cast<const uint16_t*>(y), residual, moe_out, h_out, gamma, norm_hi, norm_lo, T, eps);
-      PF_HIP(hipGetLastError());
-      return;
-    }
-  }
   const dim3 grid((T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
   if (Y16 || (D <= 768 && K == 4)) {  // the model's shape (fp16 expert outputs are built for it only)
     PF_CHECK(K == 4 && D <= 768, "moe_combine: fp16 expert outputs are built for K = 4, D <= 768");
