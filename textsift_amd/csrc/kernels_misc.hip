@@ -633,45 +633,73 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_counts(const int32_t* __rest
                                                            int32_t* __restrict__ num_tiles, int T, int K, int E,
                                                            int tile_t) {
   __shared__ uint32_t bits[256 * BWS];
-  __shared__ int32_t psum[2][RBLK];  // per (quarter of the tiles, expert): all tiles, tiles before the block
+  __shared__ int32_t psum[2][4 * RBLK];  // per (part of the tiles, expert): all tiles, tiles before the block
   __shared__ int32_t off[256], ebase[256], toff[256], wsum[2][RBLK / 64];
   __shared__ uint16_t pre[256 * BWS];
   const int blk = blockIdx.x, t0 = blk * RBLK, ntok = min(RBLK, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // Per-expert sums over the tiles, in G parts of the tile range. With E a
+  // multiple of 4 a thread loads 16 bytes (4 experts' counts) per tile:
+  // E2 / 4 expert groups x G = 4 RBLK / E2 parts; otherwise one expert per
+  // thread: E2 experts x G = RBLK / E2 parts (E2: E rounded up to 64, 128 or
+  // 256). Loads are issued 16 at a time with addresses clamped into the
+  // array and values past the range dropped.
+  const int E2 = E <= 64 ? 64 : (E <= 128 ? 128 : 256);
+  const bool vec = (E & 3) == 0;
+  const int G = vec ? 4 * RBLK / E2 : RBLK / E2;
   {
-    const int e = tid & 255, q = tid >> 8;  // a quarter of the tiles per thread
     const int tb = blk * ct_per_blk;
-    const int per = (n_ct + 3) / 4, lo = min(n_ct, q * per), hi = min(n_ct, lo + per);
-    int sa = 0, sb = 0;
-    if (e < E) {
-      int t = lo;
-      for (; t + 8 <= hi; t += 8) {  // independent loads in flight
-        int c[8];
+    const int lanes = vec ? E2 / 4 : E2;  // threads per part
+    const int e0 = vec ? 4 * (tid % lanes) : tid % lanes, q = tid / lanes;
+    const int per = (n_ct + G - 1) / G, lo = min(n_ct, q * per), hi = min(n_ct, lo + per);
+    int sa[4] = {0, 0, 0, 0}, sb[4] = {0, 0, 0, 0};
+    if (vec) {
+      const int ec = min(e0, E - 4);
+      for (int t = lo; t < hi; t += 16) {
+        int4 c[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) c[u] = counts[(size_t)(t + u) * E + e];
+        for (int u = 0; u < 16; ++u)
+          c[u] = *reinterpret_cast<const int4*>(counts + (size_t)min(t + u, n_ct - 1) * E + ec);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          sa += c[u];
-          sb += t + u < tb ? c[u] : 0;
+        for (int u = 0; u < 16; ++u) {
+          const bool in = t + u < hi && e0 < E, before = t + u < tb;
+          const int v[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            sa[i] += in ? v[i] : 0;
+            sb[i] += in && before ? v[i] : 0;
+          }
         }
       }
-      for (; t < hi; ++t) {
-        const int c = counts[(size_t)t * E + e];
-        sa += c;
-        sb += t < tb ? c : 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        psum[0][q * E2 + e0 + i] = sa[i];
+        psum[1][q * E2 + e0 + i] = sb[i];
       }
+    } else {
+      const int ec = min(e0, E - 1);
+      for (int t = lo; t < hi; t += 16) {
+        int c[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) c[u] = counts[(size_t)min(t + u, n_ct - 1) * E + ec];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int v = t + u < hi && e0 < E ? c[u] : 0;
+          sa[0] += v;
+          sb[0] += t + u < tb ? v : 0;
+        }
+      }
+      psum[0][q * E2 + e0] = sa[0];
+      psum[1][q * E2 + e0] = sb[0];
     }
-    psum[0][tid] = sa;
-    psum[1][tid] = sb;
   }
   moe_block_bitmap(idx, bits, t0, ntok, K, E);  // (its barriers also publish psum)
   // rows c and tiles n of expert e = tid; inclusive scans within the wave
   int c = 0, below = 0;
   if (tid < E) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c += psum[0][q * 256 + tid];
-      below += psum[1][q * 256 + tid];
+    for (int q = 0; q < G; ++q) {
+      c += psum[0][q * E2 + tid];
+      below += psum[1][q * E2 + tid];
     }
   }
   const int n = (c + tile_t - 1) / tile_t;
