@@ -473,6 +473,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
           if (route_counts) a.topk_counts = plan.tile_counts;  // per router tile: the routing plan's counts
+          if (!m->taps) a.out = nullptr;  // the logits stay in LDS (written only for the debug taps)
         }
         gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, router_tile, 2, "gemm_router");
       } else {

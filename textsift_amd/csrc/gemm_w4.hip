@@ -467,7 +467,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         const int byte = ((up ^ (row & SO::SWM)) << 4);
         const int w = byte / (SO::FG * SO::FB), within = byte % (SO::FG * SO::FB);
         const int col = ocol0 + (w * WF + ps * SO::FG) * SO::CF + within / SO::ESZ;
-        if (row < rows && col < oN)
+        // (the top-k epilogue may be given no logits output: it reads them from LDS)
+        if (row < rows && col < oN && (EPI != Epi::F32_TOPK || p.out))
           *reinterpret_cast<u4_t*>(static_cast<char*>(p.out) + ((size_t)(row0 + row) * p.ldo + col) * SO::ESZ) =
               *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
       }
@@ -745,7 +746,7 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
              const char* prof_name) {
   PF_CHECK(a.K > 0 && a.K % KC == 0, "gemm_w4: K must be a positive multiple of 128");
   PF_CHECK(a.N > 0, "gemm_w4: N must be positive");
-  PF_CHECK(a.x && a.w && a.wsz && a.out, "gemm_w4: null operand");
+  PF_CHECK(a.x && a.w && a.wsz && (a.out || epi == Epi::F32_TOPK), "gemm_w4: null operand");
   PF_CHECK(a.ldx % 8 == 0, "gemm_w4: activation row stride must allow 16-byte loads");
   PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
            "gemm_w4: activations and weights must be 16-byte aligned");
