@@ -116,15 +116,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int PLANE = BT * KC;    // halves per plane per buffer
 
   extern __shared__ __attribute__((aligned(16))) _Float16 xs_lds[];  // [2][XS][BT][KC] swizzled
-  // top-k epilogue: the tile's rows per expert (cleared here; barriers follow before use)
-  __shared__ int topk_hist[EPI == Epi::F32_TOPK ? 128 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-  if constexpr (EPI == Epi::F32_TOPK)
-    if (p.topk_counts && tid < 128) topk_hist[tid] = 0;
 
   const int n_tiles = (p.N + BN - 1) / BN;
   // Grouped: the grid covers the largest possible tile list; only the first
@@ -442,9 +438,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         }
       }
     }
+    // top-k epilogue: the tile's rows per expert, in LDS after the staged
+    // tile (inside the activation buffers, free now), cleared here
+    [[maybe_unused]] int* topk_hist = reinterpret_cast<int*>(ob + SO::LDS);
 #pragma unroll
     for (int ps = 0; ps < SO::NP; ++ps) {
       __syncthreads();  // every wave is done with the LDS buffers (and the previous pass)
+      if constexpr (EPI == Epi::F32_TOPK)
+        if (ps == 0 && p.topk_counts && tid < 128) topk_hist[tid] = 0;
 #pragma unroll
       for (int fl = 0; fl < SO::FG; ++fl) {
         const int f = ps * SO::FG + fl;
@@ -643,8 +644,11 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   // activation buffers: two (double buffering) or all CT chunks, plus the
   // RoPE table's plane when every chunk buffer is taken
   constexpr int NBUF = CT > 0 ? (NORM ? 2 * CT : CT) + (EPI == Epi::ROPE_F16 ? 1 : 0) : 2;
+  // (the top-k epilogue keeps 128 counters after the staged tile)
   const size_t lds = std::max((size_t)NBUF * XS * BT * KC * sizeof(uint16_t),
-                              StagedOut<WF, BT, EPI, NW>::OK ? StagedOut<WF, BT, EPI, NW>::LDS : (size_t)0);
+                              StagedOut<WF, BT, EPI, NW>::OK
+                                  ? StagedOut<WF, BT, EPI, NW>::LDS + (EPI == Epi::F32_TOPK ? 128 * 4 : 0)
+                                  : (size_t)0);
   static bool attr_set = false;  // per template instance
   if (!attr_set) {
     PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>),
