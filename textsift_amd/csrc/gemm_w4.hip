@@ -153,16 +153,21 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   const int kd = K >> 3;   // dwords per packed weight row
   const int nb = K >> 5;   // quant blocks per row
 
-  // ---- weight fragment pointers (rows past N read row N-1; never stored)
-  const uint32_t* __restrict__ W = reinterpret_cast<const uint32_t*>(p.w + (size_t)expert * p.w_gs);
-  const uint32_t* __restrict__ SZ = p.wsz + (size_t)expert * p.wsz_gs;
-  const uint32_t* wptr[WF];
-  const uint32_t* sptr[WF];
+  // ---- weight fragments: buffer loads from the expert's weights and
+  // scale pairs (one descriptor each, in scalar registers) at fixed per-lane
+  // byte offsets, the chunk in the scalar offset: no address arithmetic per
+  // load (rows past N read row N-1; never stored). The host checks that the
+  // matrices' byte sizes fit the descriptors' 31-bit range.
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.w + (size_t)expert * p.w_gs), 0, p.N * kd * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(p.wsz + (size_t)expert * p.wsz_gs), 0, p.N * nb * 4, 0x00020000);
+  uint32_t woff[WF], soff[WF];
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
     const int n = min(n0 + (wave * WF + f) * 16 + l16, p.N - 1);
-    wptr[f] = W + (size_t)n * kd + lg * 4;
-    sptr[f] = SZ + (size_t)n * nb + lg;
+    woff[f] = (uint32_t)(n * kd + lg * 4) * 4u;
+    soff[f] = (uint32_t)(n * nb + lg) * 4u;
   }
 
   // ---- activation rows this lane copies (rows past the tile read the
@@ -196,8 +201,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   auto load_w = [&](int c, u4_t* wr, uint32_t* s) {
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
-      wr[f] = *reinterpret_cast<const u4_t*>(wptr[f] + c * 16);
-      s[f] = sptr[f][c * 4];
+      // chunk c: 128 values = 64 bytes of each row, and its 4 quant blocks' pairs
+      wr[f] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[f], c * 64, 0);
+      s[f] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff[f], c * 16, 0);
     }
   };
 
@@ -757,6 +763,8 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   // activation rows are addressed with 32-bit element offsets (grouped: a.M
   // slots bound every row the tile list or the row map can name)
   PF_CHECK((long)a.M * a.ldx < (1L << 31), "gemm_w4: activation offsets exceed 32 bits");
+  // the weight and scale-pair buffer descriptors hold one matrix (expert) of N x K values
+  PF_CHECK((long)a.N * a.K / 2 < (1L << 31), "gemm_w4: one weight matrix must stay below 2^31 bytes");
   if (xk == XKind::SPLIT)
     PF_CHECK(a.x_lo && (reinterpret_cast<uintptr_t>(a.x_lo) & 15) == 0, "gemm_w4: SPLIT needs an aligned lo plane");
   if (epi == Epi::SWIGLU_SPLIT || epi == Epi::SWIGLU_F16) PF_CHECK(a.N % 4 == 0, "gemm_w4: SwiGLU needs N % 4 == 0");
