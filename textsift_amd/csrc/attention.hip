@@ -557,12 +557,8 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
 }
 
 template <typename Kern>
-void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, size_t lds, int qb, int nt, bool& attr_set) {
-  if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)lds));
-    attr_set = true;
-  }
+void launch_kernel(pfhip_backend* b, const AttnArgs& a, Kern* kern, size_t lds, int qb, int nt) {
+  allow_lds(reinterpret_cast<const void*>(kern), lds);
   // few workgroups (short inputs): the query heads of a KV head are split
   // over several workgroups (the fewest that give every CU one), so they run
   // in parallel; each still stages its K/V rows once for all its heads
@@ -581,16 +577,10 @@ void launch_attn(pfhip_backend* b, const AttnArgs& a) {
   constexpr size_t LDS = AttnGeom<HD, NCH, NW>::LDS;
   static_assert(LDS <= 160 * 1024, "attention tile exceeds the LDS");
   if (a.hw_exp) {
-    if (a.mask) {
-      static bool attr_set = false;
-      launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, true>, LDS, 16 * NW, 64 * NW, attr_set);
-    } else {
-      static bool attr_set = false;
-      launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, false>, LDS, 16 * NW, 64 * NW, attr_set);
-    }
+    if (a.mask) launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, true>, LDS, 16 * NW, 64 * NW);
+    else launch_kernel(b, a, &k_banded_attention_hw<HD, NCH, NW, false>, LDS, 16 * NW, 64 * NW);
   } else {
-    static bool attr_set = false;
-    launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, LDS, 16 * NW, 64 * NW, attr_set);
+    launch_kernel(b, a, &k_banded_attention<HD, NCH, NW>, LDS, 16 * NW, 64 * NW);
   }
 }
 

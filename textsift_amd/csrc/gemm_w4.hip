@@ -655,12 +655,7 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
                               StagedOut<WF, BT, EPI, NW>::OK
                                   ? StagedOut<WF, BT, EPI, NW>::LDS + (EPI == Epi::F32_TOPK ? 128 * 4 : 0)
                                   : (size_t)0);
-  static bool attr_set = false;  // per template instance
-  if (!attr_set) {
-    PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    attr_set = true;
-  }
+  allow_lds(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>), lds);
   ProfScope ps(b, name);
   hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>), dim3((unsigned)grid), dim3(64 * NW), lds,
                      b->stream, a);
@@ -1124,12 +1119,7 @@ void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* re
   static_assert((size_t)RN_NW * RN_BT * sizeof(float) <= (size_t)RN_NB * RN_BT * KC * 2, "row sums fit the buffers");
   const size_t lds = RN_LDS;
   auto go = [&](auto kern) {
-    static std::map<const void*, bool> attr_set;  // per kernel
-    if (!attr_set[reinterpret_cast<const void*>(kern)]) {
-      PF_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)lds));
-      attr_set[reinterpret_cast<const void*>(kern)] = true;
-    }
+    allow_lds(reinterpret_cast<const void*>(kern), lds);
     ProfScope ps(b, "gemm_o_add_rmsnorm");
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * RN_NW), lds, b->stream, a, resid, gamma, h_out,
                        xn_out, eps);

@@ -75,6 +75,10 @@ struct ProfScope {
 };
 
 void prof_flush(pfhip_backend* b);  // synchronises and accumulates pending events
+// Raises kern's dynamic LDS limit to at least `bytes` on the current device
+// (once per kernel and device; thread-safe). Call before launching with
+// more than 64 KB of dynamic LDS.
+void allow_lds(const void* kern, size_t bytes);
 
 void set_err(char* err, size_t cap, const std::string& msg);
 

@@ -58,6 +58,20 @@ void prof_flush(pfhip_backend* b) {
   b->pending.clear();
 }
 
+// ---------------------------------------------------------------- kernel attributes
+
+void pf::allow_lds(const void* kern, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> limit;  // (kernel, device) -> bytes set
+  int dev = 0;
+  PF_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  size_t& cur = limit[{kern, dev}];
+  if (cur >= bytes) return;
+  PF_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+  cur = bytes;
+}
+
 // ---------------------------------------------------------------- scratch
 
 struct Scratch {
