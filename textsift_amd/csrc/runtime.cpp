@@ -60,7 +60,7 @@ void prof_flush(pfhip_backend* b) {
 
 // ---------------------------------------------------------------- kernel attributes
 
-void pf::allow_lds(const void* kern, size_t bytes) {
+void allow_lds(const void* kern, size_t bytes) {
   static std::mutex mu;
   static std::map<std::pair<const void*, int>, size_t> limit;  // (kernel, device) -> bytes set
   int dev = 0;
