@@ -331,11 +331,20 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention(AttnArgs a) {
 // scale > 0 (the row maximum is taken over the unscaled scores).
 // max(a, b, c) in one v_max3_f32. Written as assembly: the compiler's
 // fmaxf quiets each operand first (signalling NaNs), which MFMA results and
-// -inf never are.
+// -inf never are. Its operands are MFMA results, and the compiler counts the
+// wait states before a read of those only for instructions it can see: the
+// scores pass through mfma_settled first.
 __device__ __forceinline__ float max3_f32(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
+}
+
+// Twelve wait states after the MFMAs that wrote x and y (ordered after them
+// by the operands): enough for a dependent read of an MFMA result on
+// gfx950 by instructions the compiler does not see.
+__device__ __forceinline__ void mfma_settled(f4_t& x, f4_t& y) {
+  asm volatile("s_nop 7\n\ts_nop 3" : "+v"(x), "+v"(y));
 }
 
 // MASKED: a key mask is given (a compile-time choice, so the unmasked
@@ -454,6 +463,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
               s[c][kt][r] = valid ? s[c][kt][r] : -INFINITY;
             }
         }
+        mfma_settled(s[c][0], s[c][1]);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           mr = max3_f32(mr, s[c][kt][0], s[c][kt][1]);

@@ -230,11 +230,11 @@ __device__ __forceinline__ float swiglu_clamp_fast(float gate_raw, float up_raw)
 // one fp16 ulp (plus the reference polynomial's own error, ~1e-4 relative,
 // which the GPU paths do not have).
 __device__ __forceinline__ float swiglu_clamp_hw(float gate_raw, float up_raw) {
-  // min(gate, 7) as one v_min_f32: the compiler's fminf first quiets the
-  // operand (an extra instruction per value), which accumulator values never
-  // need; a quiet NaN still yields 7, as fminf does
-  float gate;
-  asm("v_min_f32 %0, 0x40e00000, %1" : "=v"(gate) : "v"(gate_raw));
+  // min(gate, 7) with fminf (a quiet NaN yields 7). Not as inline assembly:
+  // the operands are MFMA results, which the matrix cores write several
+  // cycles after the instruction issues, and the compiler inserts those wait
+  // states only before the instructions it can see.
+  const float gate = fminf(gate_raw, 7.0f);
   const float up = __builtin_amdgcn_fmed3f(up_raw, -7.0f, 7.0f);
   constexpr float NEG_ALPHA_LOG2E = -1.702f * 1.44269504088896340736f;
   const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gate * NEG_ALPHA_LOG2E));
