@@ -340,12 +340,6 @@ __device__ __forceinline__ float max3_f32(float a, float b, float c) {
   return r;
 }
 
-// Twelve wait states after the MFMAs that wrote x and y (ordered after them
-// by the operands): enough for a dependent read of an MFMA result on
-// gfx950 by instructions the compiler does not see.
-__device__ __forceinline__ void mfma_settled(f4_t& x, f4_t& y) {
-  asm volatile("s_nop 7\n\ts_nop 3" : "+v"(x), "+v"(y));
-}
 
 // MASKED: a key mask is given (a compile-time choice, so the unmasked
 // kernel carries no per-slot mask code)
@@ -463,7 +457,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
               s[c][kt][r] = valid ? s[c][kt][r] : -INFINITY;
             }
         }
-        mfma_settled(s[c][0], s[c][1]);
+        mfma_settled(s[c]);
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           mr = max3_f32(mr, s[c][kt][0], s[c][kt][1]);

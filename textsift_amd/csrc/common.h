@@ -229,16 +229,36 @@ __device__ __forceinline__ float swiglu_clamp_fast(float gate_raw, float up_raw)
 // which changes an fp16-rounded output in about one case in a thousand, by
 // one fp16 ulp (plus the reference polynomial's own error, ~1e-4 relative,
 // which the GPU paths do not have).
+// SETTLED: the operands are MFMA results that have passed through
+// mfma_settled (below), so min(gate, 7) can be one v_min_f32 in inline
+// assembly (fminf first quiets its operand, one more instruction per value,
+// which MFMA results never need; a quiet NaN yields 7 either way). Otherwise
+// fminf: the matrix cores write a result several cycles after the MFMA
+// issues, and the compiler inserts those wait states only before the
+// instructions it can see.
+template <bool SETTLED = false>
 __device__ __forceinline__ float swiglu_clamp_hw(float gate_raw, float up_raw) {
-  // min(gate, 7) with fminf (a quiet NaN yields 7). Not as inline assembly:
-  // the operands are MFMA results, which the matrix cores write several
-  // cycles after the instruction issues, and the compiler inserts those wait
-  // states only before the instructions it can see.
-  const float gate = fminf(gate_raw, 7.0f);
+  float gate;
+  if constexpr (SETTLED) asm("v_min_f32 %0, 0x40e00000, %1" : "=v"(gate) : "v"(gate_raw));
+  else gate = fminf(gate_raw, 7.0f);
   const float up = __builtin_amdgcn_fmed3f(up_raw, -7.0f, 7.0f);
   constexpr float NEG_ALPHA_LOG2E = -1.702f * 1.44269504088896340736f;
   const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gate * NEG_ALPHA_LOG2E));
   return (up + 1.0f) * (gate * sig);
+}
+
+// Eight wait states after the MFMAs that wrote the n accumulators (the
+// operands order it after them): what a dependent read of an MFMA result
+// needs on gfx950 from an instruction the compiler does not see.
+template <int N>
+__device__ __forceinline__ void mfma_settled(f4_t (&a)[N]) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8, "1, 2, 4 or 8 accumulators");
+  if constexpr (N == 1) asm volatile("s_nop 7" : "+v"(a[0]));
+  if constexpr (N == 2) asm volatile("s_nop 7" : "+v"(a[0]), "+v"(a[1]));
+  if constexpr (N == 4) asm volatile("s_nop 7" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
+  if constexpr (N == 8)
+    asm volatile("s_nop 7"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]));
 }
 
 // v_mfma_f32_16x16x32_f16 (gfx950). Operand layout (lane l, i = l / 16):

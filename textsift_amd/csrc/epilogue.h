@@ -170,9 +170,10 @@ __device__ __forceinline__ u2_t to_f16x4_native(const float v[4]) {
   const h2_t b = __builtin_convertvector(f2_t{f32_fence(v[2]), f32_fence(v[3])}, h2_t);
   return u2_t{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
+template <bool SETTLED = false>
 __device__ __forceinline__ uint32_t swiglu_f16x2_native(const float v[4]) {
-  const float g0 = swiglu_clamp_hw(v[0], v[1]);
-  const float g1 = swiglu_clamp_hw(v[2], v[3]);
+  const float g0 = swiglu_clamp_hw<SETTLED>(v[0], v[1]);
+  const float g1 = swiglu_clamp_hw<SETTLED>(v[2], v[3]);
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{f32_fence(g0), f32_fence(g1)}, h2_t));
 }
 

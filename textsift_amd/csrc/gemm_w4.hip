@@ -406,6 +406,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   } else {
     compute((C - 1) & 1, wraw, sz);
   }
+  // the SwiGLU epilogue's clamp reads the accumulators with inline assembly
+  if constexpr (EPI == Epi::SWIGLU_F16) {
+#pragma unroll
+    for (int f = 0; f < WF; ++f) mfma_settled(acc[f]);
+  }
   if constexpr (EPI == Epi::ROPE_F16) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
           } else if constexpr (EPI == Epi::F16) {
             ow[f][tj] = to_f16x4_native(v);
           } else {
-            ow[f][tj] = u2_t{swiglu_f16x2_native(v), 0u};
+            ow[f][tj] = u2_t{swiglu_f16x2_native<true>(v), 0u};
           }
         }
       }
@@ -630,7 +635,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         store_f16x4(p, orow, n, to_f16x4_native(v));
       } else if constexpr (EPI == Epi::SWIGLU_F16) {
         *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + orow * p.ldo + (n >> 1)) =
-            swiglu_f16x2_native(v);
+            swiglu_f16x2_native<true>(v);
       } else {
         store_out<EPI>(p, orow, n, v);
       }
