@@ -12,6 +12,9 @@ ROCm toolchain) and scanned for instruction forms the kernels must not use:
     instances, whose products (fp16 x fp16) are exact in f32. v_fma_mix_f32
     (an f32 result) widens its fp16 operands exactly and rounds once to f32:
     it is the f32 fma of the widened values and is allowed anywhere;
+  * an LDS DMA (global_load_lds) in the cycle after the write of M0 that
+    holds its LDS address: it needs one wait state in between (the
+    compiler's own sequences always have one);
   * reads of an MFMA result too soon after the MFMA: the matrix cores write
     the result several cycles after the instruction issues and the hardware
     does not stall a dependent read, so it needs wait states (8 for the
@@ -195,4 +198,15 @@ def test_mfma_results_read_after_wait_states(disassembly):
     for asm in disassembly:
         for f, ins in _instructions(asm).items():
             bad += [(f[:80],) + b for b in _early_mfma_reads(ins)]
+    assert not bad, bad[:10]
+
+
+def test_lds_dma_after_m0_write(disassembly):
+    """No LDS DMA directly after an instruction that writes M0."""
+    bad = []
+    for asm in disassembly:
+        for f, ins in _instructions(asm).items():
+            for (_, a), (_, b) in zip(ins, ins[1:]):
+                if re.match(r"^s_\w+ m0,", a) and b.startswith("global_load_lds"):
+                    bad.append((f[:80], a, b))
     assert not bad, bad[:10]

@@ -845,9 +845,11 @@ constexpr size_t RN_LDS = (size_t)RN_NB * RN_BT * KC * 2 + (size_t)RN_BT * RN_BN
 // copy16_to_lds issued as inline assembly: the compiler then does not know
 // that it writes LDS and does not make every workgroup barrier wait for all
 // such copies in flight (vmcnt(0)); the kernel waits for the ones it needs
-// itself. Clobbers M0, which nothing else in the kernel uses.
+// itself. Clobbers M0, which nothing else in the kernel uses. An LDS DMA
+// reads M0 one wait state after the write at the earliest (the s_nop).
 __device__ __forceinline__ void copy16_to_lds_async(const void* src, uint32_t lds_byte) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_byte) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_byte)
+               : "memory", "m0");
 }
 
 // C = K / 128 chunks, fully unrolled: chunk c + 2 is loaded while chunk c
