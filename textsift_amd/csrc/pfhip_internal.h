@@ -170,9 +170,11 @@ void gemm_w4_add_rmsnorm(pfhip_backend* b, const GemmArgs& a, const uint16_t* re
 void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const uint8_t* wz, uint32_t* w_out,
                 uint32_t* sz_out, int rows, int K);
 
-// GatherBlockQuantized embedding: out fp16 [T][D].
+// GatherBlockQuantized embedding: out fp16 [T][D]. stream_out: non-temporal
+// stores (the output is not read by the next kernel: the stand-alone op);
+// the forward keeps them cached for the RMSNorm that reads them next.
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
-                  uint16_t* out, int T, int V, int D);
+                  uint16_t* out, int T, int V, int D, bool stream_out = false);
 
 // RMSNorm family. The *_split variants write the f32 result as hi/lo fp16
 // planes (norm_hi, norm_lo) for SPLIT GEMM inputs.

@@ -272,7 +272,7 @@ static std::vector<KernelEntry>& registry() {
                  need(bs, 3, (size_t)T * 4, "embed_lookup_int4");
                  need(bs, 4, (size_t)T * D * 2, "embed_lookup_int4");
                  embed_lookup(b, bp<uint8_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint8_t>(bs, 2), bp<int32_t>(bs, 3),
-                              bp<uint16_t>(bs, 4), T, V, D);
+                              bp<uint16_t>(bs, 4), T, V, D, /*stream_out=*/true);
                }});
   r.push_back({"matmul_int4_fp16_f16", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  run_matmul(b, bs, p, false, false, "matmul_int4_fp16_f16");
