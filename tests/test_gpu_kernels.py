@@ -447,7 +447,8 @@ def test_router_topk_fixture(be, fixture):
 # (T <= 1024: the one-workgroup route kernel)
 @pytest.mark.parametrize("T,E,tile", [(2048, 128, 64), (1, 128, 64), (32768, 128, 128), (1000, 8, 128),
                                       (300, 128, 16), (1024, 128, 16), (1025, 128, 64), (64, 128, 16), (200, 8, 64),
-                                      (7, 200, 16), (5000, 256, 128)])
+                                      (7, 200, 16), (5000, 256, 128), (2049, 128, 64), (1500, 256, 16),
+                                      (1111, 8, 128)])
 def test_moe_route_permutation_bit_exact(be, T, E, tile):
     K = 4
     rng = np.random.default_rng(T + E)
