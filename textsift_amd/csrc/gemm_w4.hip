@@ -480,9 +480,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         const int w = byte / (SO::FG * SO::FB), within = byte % (SO::FG * SO::FB);
         const int col = ocol0 + (w * WF + ps * SO::FG) * SO::CF + within / SO::ESZ;
         // (the top-k epilogue may be given no logits output: it reads them from LDS)
-        if (row < rows && col < oN && (EPI != Epi::F32_TOPK || p.out))
-          *reinterpret_cast<u4_t*>(static_cast<char*>(p.out) + ((size_t)(row0 + row) * p.ldo + col) * SO::ESZ) =
-              *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
+        if (row < rows && col < oN && (EPI != Epi::F32_TOPK || p.out)) {
+          u4_t* dstp =
+              reinterpret_cast<u4_t*>(static_cast<char*>(p.out) + ((size_t)(row0 + row) * p.ldo + col) * SO::ESZ);
+          const u4_t val = *reinterpret_cast<const u4_t*>(ob + row * SO::PRB + (up << 4));
+          // the expert outputs (grouped fp16: the down GEMM) are read once,
+          // by the combine: non-temporal stores (down 150 -> 144 us)
+          if constexpr (GROUPED && EPI == Epi::F16) __builtin_nontemporal_store(val, dstp);
+          else *dstp = val;
+        }
       }
     }
     if constexpr (EPI == Epi::F32_TOPK && SO::NP == 1 && BN == 128) {
