@@ -366,7 +366,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       __syncthreads();
       load_x(c + 1, (c & 1) ^ 1);
       load_w(c + 1, wnext, sznext);
+      // the expert GEMMs raise the wave's issue priority over the chunk's
+      // MFMAs and dequantisation (and drop it for the loads and the barrier):
+      // gate_up 235 -> 229 us, down -1 us; the dense QKV GEMM got slower with it
+      if constexpr (GROUPED) __builtin_amdgcn_s_setprio(1);
       compute(c & 1, wraw, sz);
+      if constexpr (GROUPED) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int f = 0; f < WF; ++f) {
         wraw[f] = wnext[f];
