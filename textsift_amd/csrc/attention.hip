@@ -517,6 +517,9 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
       for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x32(vf[dt], pf, o[dt]);
       lsum = mfma16x16x32(ones, pf, lsum);
     };
+    // pass 2 (exponentials and P.V) at raised wave priority: the waves in it
+    // issue ahead of those in the max pass (-1.7 us)
+    __builtin_amdgcn_s_setprio(1);
     load_v(0, vb[0]);
     if (!empty(0) && !empty(NCH - 1)) {
       // every chunk has keys (all but the sequence ends): one branch-free
@@ -543,6 +546,7 @@ __global__ __launch_bounds__(64 * NW) void k_banded_attention_hw(AttnArgs a) {
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     const float l = lsum[0] + __builtin_amdgcn_exp2f(sink2 - m);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     // lane holds out[tq][hq*HD + 16 dt + 4 lg + r]
