@@ -335,14 +335,15 @@ REF_LATENCY_MS = {7: {"WebGPU M3 Pro": 8.9, "Metal M2 Pro": 5.2}, 25: {"WebGPU M
                   32: {"Metal M2 Pro": 10.8}, 80: {"WebGPU M3 Pro": 22.0, "Metal M2 Pro": 23.8}}
 
 
-def latency_table(model, cfg, reps=50):
-    """Median latency of one B=1 forward at each published T: host token ids
-    in, host f32 logits out (copies included), and device-resident."""
+def latency_measure(model, cfg, Ts=(7, 25, 32, 80), reps=50, weights=None, cpu_threads_n=0):
+    """Median latency (ms) of one B=1 forward at each T: device-resident
+    (token ids and logits in HBM) and host in/out (copies included), after 5
+    warmups; with `weights`, also the oracle forward on the host (median of 3
+    after one warmup, cpu_threads_n threads). {T: {"dev", "host"[, "cpu"]}}"""
     from textsift_amd import synth
-    rows = ["| T | host in/out ms (median) | device-resident ms (median) | reference (other hardware) |",
-            "|---|---|---|---|"]
-    for T in sorted(REF_LATENCY_MS):
-        ids = synth.token_ids(7 + T, T, cfg.vocab_size)
+    out = {}
+    for T in Ts:
+        ids = synth.tagged_token_ids(7 + T, T, cfg.vocab_size)
         mask = np.ones(T, np.uint8)
         for _ in range(5):
             model.forward(ids, mask, 1, T)
@@ -353,6 +354,8 @@ def latency_table(model, cfg, reps=50):
             host.append((time.perf_counter() - t0) * 1000.0)
         be = model.backend
         ib, lb = be.buffer(ids), be.buffer(nbytes=T * cfg.num_classes * 4)
+        for _ in range(3):
+            model.forward_device(ib, None, 1, T, lb)
         dev = []
         for _ in range(reps):
             t0 = time.perf_counter()
@@ -360,8 +363,29 @@ def latency_table(model, cfg, reps=50):
             dev.append((time.perf_counter() - t0) * 1000.0)
         ib.release()
         lb.release()
+        out[T] = {"dev": round(float(np.median(dev)), 4), "host": round(float(np.median(host)), 4)}
+        if weights is not None:
+            import oracle
+            nt = cpu_threads_n or 1
+            oracle.model_forward(cfg, weights, ids, n_threads=nt)
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                oracle.model_forward(cfg, weights, ids, n_threads=nt)
+                ts.append((time.perf_counter() - t0) * 1000.0)
+            out[T]["cpu"] = round(float(np.median(ts)), 2)
+    return out
+
+
+def latency_table(model, cfg, reps=50):
+    """Markdown table of latency_measure at the token counts the reference
+    publishes, next to its published numbers (other hardware)."""
+    rows = ["| T | host in/out ms (median) | device-resident ms (median) | reference (other hardware) |",
+            "|---|---|---|---|"]
+    lat = latency_measure(model, cfg, tuple(sorted(REF_LATENCY_MS)), reps)
+    for T in sorted(REF_LATENCY_MS):
         ref = ", ".join(f"{k} {v} ms" for k, v in REF_LATENCY_MS[T].items())
-        rows.append(f"| {T} | {np.median(host):.3f} | {np.median(dev):.3f} | {ref} |")
+        rows.append(f"| {T} | {lat[T]['host']:.3f} | {lat[T]['dev']:.3f} | {ref} |")
     return "\n".join(rows)
 
 
@@ -478,9 +502,9 @@ def roof(achieved, peak, unit, traffic=None):
 
 
 def bench_config(cfg_id, reps, variant="both", no_cpu=False, calib_mb=0):
-    """One JSON line for BASELINE config 1-4 (each kernel on its own, cache-warm
-    and cache-cold), with the roofline against MI355X peaks and the oracle CPU
-    baseline at both thread settings."""
+    """BASELINE config 1-4 (each kernel on its own, cache-warm and cache-cold),
+    with the roofline against MI355X peaks and the oracle CPU baseline at both
+    thread settings: the dict of one JSON line."""
     import oracle
     from textsift_amd import _native, synth
     from textsift_amd.config import PF_CONFIG as cfg
@@ -714,7 +738,27 @@ def bench_config(cfg_id, reps, variant="both", no_cpu=False, calib_mb=0):
     for b_ in keep:
         b_.release()
     be.close()
-    print(json.dumps(out))
+    return out
+
+
+def config_summary(out):
+    """The compact per-config record the headline line carries: kernel time
+    (median of the reference's method, us) warm and HBM-cold, the cold roofline
+    fraction and its bound, the CPU baseline at all cores and at the
+    reference's default thread count, and the parity check's result."""
+    cpu = out.get("cpu_baseline")
+    parity = ("bit-exact" if out.get("bit_exact_vs_oracle") else "NOT bit-exact") \
+        if "bit_exact_vs_oracle" in out else f"rel-err {out.get('rel_err_vs_oracle', float('nan')):.2e}"
+    rec = {"us": [out["warm"]["median_us"], out["cold"]["median_us"]],
+           "frac": out["roofline"]["frac"], "bound": out["roofline"]["bound"],
+           "roofline_us": out["roofline_time_us"], "parity": parity}
+    if "mfma" in out["cold"]:
+        rec["mfma_frac"] = out["cold"]["mfma"]["frac"]
+    if cpu:
+        rec["cpu"] = [cpu["value"], cpu["reference_default_threads"]["value"], cpu["unit"]]
+    if "zipf" in out:
+        rec["launches"] = len(out["config"]["kernels"])
+    return rec
 
 
 def main():
@@ -749,6 +793,11 @@ def main():
                     help="print a table of each forward GEMM next to a dense fp16 torch.matmul (hipBLASLt) of "
                          "the same M x N x K, then exit")
     ap.add_argument("--blas-torch", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--recipe", choices=["spread", "uniform"], default="spread",
+                    help="synthetic weights (textsift_amd.synth.make_model_weights): spread (the default) or the "
+                         "earlier uniform recipe, whose routing collapses")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="config 5 only: skip the small-T latencies, the collapsed-model comparison and configs 1-4")
     ap.add_argument("--latency", action="store_true",
                     help="single-sequence forward latency at the token counts the reference publishes, then exit")
     args = ap.parse_args()
@@ -782,7 +831,7 @@ def main():
         sys.exit(2)
 
     if args.config != 5:
-        bench_config(args.config, args.reps, args.variant, args.no_cpu, args.copy_calibration_mb)
+        print(json.dumps(bench_config(args.config, args.reps, args.variant, args.no_cpu, args.copy_calibration_mb)))
         return
 
     from textsift_amd import _native, synth
@@ -792,16 +841,13 @@ def main():
     B, T = args.batch, args.seq
     M = B * T
     t_gen = time.time()
-    weights = synth.make_model_weights(cfg, seed=args.seed)
-    ids = synth.token_ids(args.seed + 1, M)
+    weights = synth.make_model_weights(cfg, seed=args.seed, recipe=args.recipe)
+    ids = (synth.tagged_token_ids(args.seed + 1, M) if args.recipe == "spread" else synth.token_ids(args.seed + 1, M))
     gen_s = time.time() - t_gen
 
     be = _native.Backend(0)
     prec = _native.PRECISION_FP16 if args.precision == "fp16" else _native.PRECISION_SPLIT
-    model = _native.Model(be, cfg, precision=prec)
-    for name, arr in weights.items():
-        model.set_weight(name, arr)
-    model.finalize()
+    model = load_model(be, cfg, weights, prec)
     ids_buf = be.buffer(ids)
     logits_buf = be.buffer(nbytes=M * cfg.num_classes * 4)
 
@@ -842,9 +888,23 @@ def main():
         print(blas_reference_table(cfg, M, prof, blas_ref))
         return
 
-    # sanity: logits finite
-    logits = logits_buf.read(np.float32)
+    logits = logits_buf.read(np.float32).reshape(M, cfg.num_classes)
     finite = bool(np.isfinite(logits).all())
+    am = np.argmax(logits, 1)
+    argmax = {"classes": int(np.unique(am).size), "max_share": round(float(np.bincount(am).max() / M), 4)}
+    if args.recipe == "spread":
+        argmax["planted_tag_agreement"] = round(float(np.mean(am == ids % cfg.num_classes)), 5)
+
+    # the realised expert load per layer (one forward with the routing taps on)
+    model.enable_taps(True)
+    model.forward_device(ids_buf, None, B, T, logits_buf)
+    K, E = cfg.num_experts_per_tok, cfg.num_experts
+    loads = [synth.routing_load(model.tap(f"ridx.{l}", np.int32, M * K), E) for l in range(cfg.num_layers)]
+    model.enable_taps(False)
+    routing = {"experts_touched": [r["touched"] for r in loads],
+               "max_share": [round(r["max_share"], 4) for r in loads],
+               "top20_share": [round(r["top20_share"], 3) for r in loads],
+               "under_0p1pct": [r["under_0p1pct"] for r in loads]}
 
     # roofline of the dominant kernel
     flops = gemm_flops(cfg, M)
@@ -853,8 +913,7 @@ def main():
     kernels = {}
     if prof:
         for name, (n, ms) in prof.items():
-            kernels[name] = {"launches": n, "avg_us": round(1000.0 * ms / n, 3),
-                             "total_ms_per_step": round(ms / args.profile_steps, 4)}
+            kernels[name] = round(1000.0 * ms / n, 2)
     if dom_prof and dom in flops:
         n, ms = dom_prof
         avg_s = ms / n / 1000.0
@@ -867,6 +926,52 @@ def main():
                       ("gemm_qkv_rope", "gemm_o", "gemm_router", "gemm_moe_gate_up", "gemm_moe_down",
                        "banded_attention")) + flops["gemm_classifier"]
 
+    n_host, cpu_model = host_cpu()
+    thr = args.cpu_threads or cpu_threads()
+    refc = ref_default_threads(n_host)
+    extra = {}
+    if not args.headline_only:
+        # small T: the reference's published forward sizes, one sequence each
+        extra["latency_ms"] = {str(t): v for t, v in latency_measure(
+            model, cfg, (7, 25, 80), reps=30, weights=None if args.no_cpu else weights, cpu_threads_n=refc).items()}
+    model.close()
+    ids_buf.release()
+    logits_buf.release()
+
+    if not args.headline_only:
+        # the collapsed model of the "uniform" recipe, same batch: labelled comparison value
+        wu = synth.make_model_weights(cfg, seed=args.seed, recipe="uniform")
+        mu = load_model(be, cfg, wu, prec)
+        idu = synth.token_ids(args.seed + 1, M)
+        ib, lb = be.buffer(idu), be.buffer(nbytes=M * cfg.num_classes * 4)
+        for _ in range(args.warmup):
+            mu.forward_device(ib, None, B, T, lb)
+        steps_u = max(5, args.steps // 2)
+        t2 = time.perf_counter()
+        for _ in range(steps_u):
+            mu.forward_device(ib, None, B, T, lb)
+        ms_u = (time.perf_counter() - t2) * 1000.0 / steps_u
+        mu.enable_taps(True)
+        mu.forward_device(ib, None, B, T, lb)
+        touched_u = [synth.routing_load(mu.tap(f"ridx.{l}", np.int32, M * K), E)["touched"]
+                     for l in range(cfg.num_layers)]
+        mu.close()
+        ib.release()
+        lb.release()
+        del wu
+        extra["collapsed_model"] = {
+            "ms_per_step": round(ms_u, 3), "tokens_per_s": round(M / (ms_u / 1000.0), 1),
+            "experts_touched": touched_u,
+            "note": "earlier synthetic recipe (uniform nibbles 0-15, zp 8): routing collapses onto a few experts, "
+                    "one class for every token; not the headline"}
+    be.close()
+
+    if not args.headline_only:
+        # BASELINE configs 1-4, each kernel on its own (warm and HBM-cold), with their CPU baselines
+        extra["configs"] = {}
+        for c in (1, 2, 3, 4):
+            extra["configs"][str(c)] = config_summary(bench_config(c, args.reps, "both", args.no_cpu))
+
     cpu = None
     if not args.no_cpu:
         # the oracle (C restatement of the WASM path, the reference's MtPool
@@ -875,9 +980,6 @@ def main():
         # sequences run one after another as the reference runs its chunks, so
         # tokens/s of the sample is that of the whole 16-sequence batch
         import oracle
-        n_host, model = host_cpu()
-        thr = args.cpu_threads or cpu_threads()
-        refc = ref_default_threads(n_host)
 
         def cpu_rate(nthr, nseq):
             t2 = time.perf_counter()
@@ -889,14 +991,13 @@ def main():
         v_all, s_all = cpu_rate(thr, nseq)
         v_ref, s_ref = cpu_rate(refc, 1) if refc != thr else (v_all, 0.0)
         cpu = {"value": round(v_all, 2), "unit": "tokens/s", "cores": thr, "kind": "port",
-               "sample": f"{nseq} of the batch's {B} sequences ({nseq}x{T} tokens, same model and ids, {s_all:.1f} s) "
-                         f"through the oracle (C restatement of the WASM path, MtPool partitioning on {thr} threads); "
-                         f"the batch's sequences run serially, so this rate extrapolates to all {B}",
-               "host_nproc": n_host, "cpu_model": model,
+               "sample": f"{nseq} of the batch's {B} sequences ({nseq}x{T} tokens, {s_all:.1f} s) through the oracle "
+                         f"(C restatement of the WASM path, MtPool partitioning, {thr} threads); sequences run "
+                         f"serially, so the rate extrapolates to all {B}",
+               "host_nproc": n_host, "cpu_model": cpu_model,
                "reference_default_threads": {"cores": refc, "value": round(v_ref, 2),
                                              "sample": f"1 sequence ({T} tokens, {s_ref:.1f} s)"}}
 
-    be.close()
     out = {
         "metric": "tokens/sec full encoder fwd @16x2048; int4 GEMM % HBM/MFMA roofline",
         "value": round(tok_s, 1),
@@ -909,21 +1010,32 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4w/fp16-mfma/f32-acc" if args.precision == "fp16" else "int4w/f32-as-fp16x2-mfma/f32-acc",
-        "precision": ("fp16 (PFHIP_PRECISION_FP16: fp16 GEMM inputs, block scale folded into fp16 weights)"
-                      if args.precision == "fp16" else
-                      "split (PFHIP_PRECISION_SPLIT: f32 GEMM inputs as hi/lo fp16 planes, per-block f32 scaling)"),
-        "data": "synthetic (seeded random-init int4 weights, uniform token ids)",
+        "precision": args.precision,
+        "data": (f"synthetic: seeded random-init int4 weights ({args.recipe} recipe), token ids "
+                 + ("uniform over the vocabulary, drawn as legal BIOES runs of the ids' planted classes"
+                    if args.recipe == "spread" else "uniform")),
         "config": {"workload": "full synthetic 8-layer int4 MoE encoder forward (BASELINE config 5)",
                    "batch": B, "seq_len": T, "layers": cfg.num_layers, "experts": cfg.num_experts,
                    "topk": cfg.num_experts_per_tok, "vocab": cfg.vocab_size, "window": cfg.sliding_window},
         "roofline": roof,
         "cpu_baseline": cpu,
         "model_tflops_per_s": round(total_flops / (ms_per_step / 1000.0) / 1e12, 2),
-        "kernels": kernels,
+        "routing": routing,
+        "argmax": argmax,
+        "kernels_us": kernels,
         "logits_finite": finite,
-        "weight_gen_s": round(gen_s, 1),
     }
+    out.update(extra)
     print(json.dumps(out))
+
+
+def load_model(be, cfg, weights, prec):
+    from textsift_amd import _native
+    model = _native.Model(be, cfg, precision=prec)
+    for name, arr in weights.items():
+        model.set_weight(name, arr)
+    model.finalize()
+    return model
 
 
 if __name__ == "__main__":

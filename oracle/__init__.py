@@ -82,6 +82,8 @@ def lib():
             C.c_uint32, C.c_int]
         _lib.pfo_model_forward.argtypes = [C.POINTER(Config), C.POINTER(Model), C.c_void_p, C.c_void_p,
                                            C.c_uint32, C.c_int, C.c_void_p]
+        _lib.pfo_model_forward_route.argtypes = [C.POINTER(Config), C.POINTER(Model), C.c_void_p, C.c_void_p,
+                                                 C.c_uint32, C.c_int, C.c_void_p, C.c_void_p]
         _lib.pfo_block_forward.argtypes = [C.POINTER(Config), C.POINTER(Layer)] + [C.c_void_p] * 5 + [
             C.c_uint32, C.c_int]
     return _lib
@@ -282,8 +284,9 @@ def make_layer(keep, w, l):
                  _qw(keep, w, p + ".experts.down"))
 
 
-def model_forward(cfg, w, ids, mask=None, n_threads=1, num_layers=None):
-    """Oracle forward -> fp16 logit bits [T, classes] (WASM path, model.ts:50-105)."""
+def model_forward(cfg, w, ids, mask=None, n_threads=1, num_layers=None, return_routing=False):
+    """Oracle forward -> fp16 logit bits [T, classes] (WASM path, model.ts:50-105).
+    return_routing: also every layer's routed expert ids, int32 [layers, T, topk]."""
     L = cfg.num_layers if num_layers is None else num_layers
     E = w["layers.0.router.int4"].shape[0]
     V = w["embed.int4"].shape[0]
@@ -297,10 +300,12 @@ def model_forward(cfg, w, ids, mask=None, n_threads=1, num_layers=None):
     T = ids.size
     mask = None if mask is None else _c(mask, np.uint8)
     out = np.empty((T, cfg.num_classes), np.uint16)
-    rc = lib().pfo_model_forward(C.byref(c), C.byref(m), _p(ids), _p(mask), T, n_threads, _p(out))
+    route = np.empty((L, T, cfg.num_experts_per_tok), np.int32) if return_routing else None
+    rc = lib().pfo_model_forward_route(C.byref(c), C.byref(m), _p(ids), _p(mask), T, n_threads, _p(out),
+                                       _p(route))
     if rc != 0:
         raise RuntimeError("oracle model_forward failed")
-    return out
+    return (out, route) if return_routing else out
 
 
 def expert_dispatch(cfg, w, l, hidden_f32, ridx, rw, n_slices=1):

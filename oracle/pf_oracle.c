@@ -822,9 +822,10 @@ static void arn_slice(void* p, uint32_t t0, uint32_t tc, int w) {
   pfo_add_rmsnorm_fp16_to_f32(c->a + o, c->b + o, c->g, c->sum + o, c->norm + o, tc, c->D, c->eps);
 }
 
-int pfo_block_forward(const pfo_config* cfg, const pfo_layer* L, const uint16_t* input, uint16_t* output,
-                      const uint16_t* cos_t, const uint16_t* sin_t, const uint8_t* mask, uint32_t T,
-                      int n_threads) {
+/* ridx_out (optional, [T][K]): the layer's routed expert ids */
+static int block_forward_impl(const pfo_config* cfg, const pfo_layer* L, const uint16_t* input, uint16_t* output,
+                              const uint16_t* cos_t, const uint16_t* sin_t, const uint8_t* mask, uint32_t T,
+                              int n_threads, int32_t* ridx_out) {
   const uint32_t D = cfg->hidden, Hq = cfg->heads, Hkv = cfg->kv_heads, hd = cfg->head_dim;
   const uint32_t E = cfg->experts, K = cfg->topk;
   const int N = n_threads < 1 ? 1 : n_threads;
@@ -875,6 +876,7 @@ int pfo_block_forward(const pfo_config* cfg, const pfo_layer* L, const uint16_t*
     run_slices(mm_slice, &c, T, nT);
   }
   pfo_router_select(rl, ridx, rw, T, E, K);
+  if (ridx_out) memcpy(ridx_out, ridx, sizeof(int32_t) * (size_t)T * K);
   /* expertDispatch: MT mode always takes the sliced path (expert.ts:115-121) */
   if (pfo_expert_dispatch(cfg, L, n2, ridx, rw, moe, T, N) != 0) goto done;
   pfo_add_fp16(res2, moe, output, T * D);
@@ -885,8 +887,14 @@ done:
   return rc;
 }
 
-int pfo_model_forward(const pfo_config* cfg, const pfo_model* m, const int32_t* ids, const uint8_t* mask,
-                      uint32_t T, int n_threads, uint16_t* logits) {
+int pfo_block_forward(const pfo_config* cfg, const pfo_layer* L, const uint16_t* input, uint16_t* output,
+                      const uint16_t* cos_t, const uint16_t* sin_t, const uint8_t* mask, uint32_t T,
+                      int n_threads) {
+  return block_forward_impl(cfg, L, input, output, cos_t, sin_t, mask, T, n_threads, NULL);
+}
+
+int pfo_model_forward_route(const pfo_config* cfg, const pfo_model* m, const int32_t* ids, const uint8_t* mask,
+                            uint32_t T, int n_threads, uint16_t* logits, int32_t* ridx_out) {
   const uint32_t D = cfg->hidden, half = cfg->head_dim / 2;
   uint16_t* cs = (uint16_t*)malloc(2 * (size_t)T * half);
   uint16_t* sn = (uint16_t*)malloc(2 * (size_t)T * half);
@@ -903,7 +911,8 @@ int pfo_model_forward(const pfo_config* cfg, const pfo_model* m, const int32_t* 
   pfo_embed_lookup_int4(m->embed_int4, m->embed_scales, m->embed_zp, ids, h0, T, cfg->vocab, D);
   uint16_t *src = h0, *dst = h1;
   for (uint32_t l = 0; l < cfg->layers; l++) {
-    if (pfo_block_forward(cfg, &m->layers[l], src, dst, cs, sn, mk, T, n_threads) != 0) goto done;
+    if (block_forward_impl(cfg, &m->layers[l], src, dst, cs, sn, mk, T, n_threads,
+                           ridx_out ? ridx_out + (size_t)l * T * cfg->topk : NULL) != 0) goto done;
     uint16_t* t = src; src = dst; dst = t;
   }
   pfo_rms_norm_fp16_to_f32(src, m->final_ln, cx, T, D, cfg->eps);
@@ -913,4 +922,9 @@ int pfo_model_forward(const pfo_config* cfg, const pfo_model* m, const int32_t* 
 done:
   free(cs); free(sn); free(h0); free(h1); free(cx);
   return rc;
+}
+
+int pfo_model_forward(const pfo_config* cfg, const pfo_model* m, const int32_t* ids, const uint8_t* mask,
+                      uint32_t T, int n_threads, uint16_t* logits) {
+  return pfo_model_forward_route(cfg, m, ids, mask, T, n_threads, logits, NULL);
 }

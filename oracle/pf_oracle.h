@@ -131,6 +131,11 @@ int pfo_model_forward(const pfo_config* cfg, const pfo_model* m, const int32_t* 
                       const uint8_t* mask, uint32_t T, int n_threads, uint16_t* logits);
 
 /* One transformer block (block.ts:108-197); in/out fp16 [T, hidden]. */
+/* pfo_model_forward that also returns every layer's routed expert ids
+ * (ridx_out [layers][T][topk], NULL to skip). */
+int pfo_model_forward_route(const pfo_config* cfg, const pfo_model* m, const int32_t* ids,
+                            const uint8_t* mask, uint32_t T, int n_threads, uint16_t* logits,
+                            int32_t* ridx_out);
 int pfo_block_forward(const pfo_config* cfg, const pfo_layer* layer, const uint16_t* input,
                       uint16_t* output, const uint16_t* cos_t, const uint16_t* sin_t,
                       const uint8_t* mask, uint32_t T, int n_threads);

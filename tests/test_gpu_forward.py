@@ -10,11 +10,12 @@ import numpy as np
 import pytest
 
 import oracle
-from parity_util import f16, near_tie_only, rel_err_norm, span_parity
+from parity_util import SYNTH_OPERATING_POINT, f16, logit_spread, near_tie_only, rel_err_norm, span_parity
 from textsift_amd import _native, synth
 from textsift_amd.backend import HipBackend
 from textsift_amd.config import PF_CONFIG
-from textsift_amd.spans import ALL_SPAN_LABELS, Chunk, ViterbiDecoder, bioes_to_spans, zero_calibration
+from textsift_amd.spans import (ALL_SPAN_LABELS, Chunk, ViterbiDecoder, bioes_to_spans, load_calibration,
+                                zero_calibration)
 
 pytestmark = pytest.mark.gpu
 
@@ -57,7 +58,7 @@ def test_small_forward_vs_oracle(small, T, masked):
     err = rel_err_norm(got, ref)
     print(f"small model T={T} masked={masked}: rel-err {err:.3e}")
     assert err < 2e-3
-    assert np.mean(np.argmax(got, 1) == np.argmax(ref, 1)) >= 0.999 or T < 100
+    assert np.mean(np.argmax(got, 1) == np.argmax(ref, 1)) >= 0.999
 
 
 def test_batched_forward_equals_per_sequence(small):
@@ -134,36 +135,59 @@ def _synthetic_chunk(T):
     return Chunk(np.zeros(T, np.int32), np.ones(T, np.uint8), list(range(0, 2 * T + 1, 2)), "ab" * T, 0, (0, T))
 
 
+SYNTH_CAL = load_calibration(SYNTH_OPERATING_POINT)
+CALIBRATIONS = (("zero", None), ("synthetic operating point", SYNTH_CAL))
+
+
 @pytest.fixture(scope="module")
 def full_ref():
-    """Oracle logits of the full-size model for one T=2048 sequence."""
+    """Oracle logits and routing of the full-size model for one T=2048
+    sequence of tagged ids (synth.tagged_token_ids: a legal BIOES sequence of
+    the ids' planted classes). The synthetic model must not be degenerate, or
+    the argmax and span checks below prove nothing: the oracle's argmax uses
+    at least 10 classes with none above 30 %, and its spans include
+    multi-token runs under both calibrations."""
     T = 2048
     w = synth.make_model_weights(PF_CONFIG, seed=20260101)
-    ids = synth.token_ids(1000, T)
-    ref = f16(oracle.model_forward(PF_CONFIG, w, ids, n_threads=8)).astype(np.float32)
-    return w, ids, ref
+    ids = synth.tagged_token_ids(1000, T)
+    bits, route = oracle.model_forward(PF_CONFIG, w, ids, n_threads=8, return_routing=True)
+    ref = f16(bits).astype(np.float32)
+    classes, top = logit_spread(ref)
+    print(f"oracle argmax: {classes} classes, largest share {top:.3f}")
+    assert classes >= 10 and top <= 0.30
+    for name, cal in CALIBRATIONS:
+        _, rep = span_parity(ref, ref, _synthetic_chunk(T), calibration=cal)
+        print(f"oracle spans ({name} calibration): {rep['n_spans']}, multi-token {rep['multi_token_spans']}")
+        assert rep["multi_token_spans"] >= 10
+    return w, ids, ref, route
+
+
+def _check_logits(got, ref, what):
+    T = ref.shape[0]
+    err = rel_err_norm(got, ref)
+    agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
+    print(f"{what}: rel-err {err:.3e}, argmax agreement {agree:.5f} ({int(round((1 - agree) * T))} tokens differ)")
+    assert err < 2e-3
+    assert agree >= 0.999
+    for name, cal in CALIBRATIONS:
+        same, rep = span_parity(got, ref, _synthetic_chunk(T), calibration=cal)
+        print(f"  spans ({name} calibration): identical {same} {rep}")
+        assert same or near_tie_only(rep, T)
 
 
 @pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
 def test_full_model_forward_vs_oracle(full_ref, precision):
     """BASELINE config 5 architecture at full size (8 layers, 128 experts,
     vocab 200064), one T=2048 sequence (the reference's chunk length)."""
-    w, ids, ref = full_ref
+    w, ids, ref, _ = full_ref
     T = ids.size
     be = HipBackend(w, precision=precision)
     be.warmup()
     try:
         got = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
-        err = rel_err_norm(got, ref)
-        agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
-        same, rep = span_parity(got, ref, _synthetic_chunk(T))
-        print(f"full model T={T} precision={precision}: rel-err {err:.3e}, argmax agreement {agree:.5f}, "
-              f"spans identical {same} {rep}")
-        assert err < 2e-3
-        assert agree >= 0.999
-        assert same or near_tie_only(rep, T)
     finally:
         be.dispose()
+    _check_logits(got, ref, f"full model T={T} precision={precision}")
 
 
 @pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
@@ -177,10 +201,10 @@ def test_full_batch_16x2048(full_ref, precision):
     logits also equal those of its own single-sequence forward (2048 rows:
     the O GEMM with the norm in the router's 16-row tile, 64-row expert
     tiles) bit for bit, so no result depends on the batch it was run in."""
-    w, ids0, ref0 = full_ref
+    w, ids0, ref0, _ = full_ref
     T = ids0.size
     B = 16
-    ids = synth.token_ids(1016, B * T).reshape(B, T)
+    ids = synth.tagged_token_ids(1016, B * T).reshape(B, T)
     ids[0] = ids0
     be = HipBackend(w, precision=precision)
     be.warmup()
@@ -197,14 +221,39 @@ def test_full_batch_16x2048(full_ref, precision):
         be.dispose()
     ref15 = f16(oracle.model_forward(PF_CONFIG, w, ids[15], n_threads=8)).astype(np.float32)
     for b, ref in ((0, ref0), (15, ref15)):
-        err = rel_err_norm(got[b], ref)
-        agree = np.mean(np.argmax(got[b], 1) == np.argmax(ref, 1))
-        same, rep = span_parity(got[b], ref, _synthetic_chunk(T))
-        print(f"16x2048 precision={precision} sequence {b}: rel-err {err:.3e}, argmax agreement {agree:.5f}, "
-              f"spans identical {same} {rep}")
-        assert err < 2e-3
-        assert agree >= 0.999
-        assert same or near_tie_only(rep, T)
+        _check_logits(got[b], ref, f"16x2048 precision={precision} sequence {b}")
+
+
+def test_full_model_routing_load(full_ref):
+    """The synthetic model's realised expert load at the benchmarked 16x2048
+    batch (GPU routing taps, fp16 numerics) sits where openai/privacy-filter's
+    measured routing does (docs/stage3-gate-measurement.md:35-55:
+    no expert above 10 %, the top 20 % of experts take 43-58 % of the picks,
+    0-2 experts under 0.1 %), in every layer; and the GPU's routing of
+    sequence 0 is the oracle's for all but near-tied picks."""
+    w, ids0, _, route0 = full_ref
+    B, T, K, E = 16, ids0.size, PF_CONFIG.num_experts_per_tok, PF_CONFIG.num_experts
+    ids = synth.tagged_token_ids(1016, B * T).reshape(B, T)
+    ids[0] = ids0
+    be = HipBackend(w)
+    be.warmup()
+    m = be.model
+    m.enable_taps(True)
+    try:
+        be.forward_batch(ids)
+        for l in range(PF_CONFIG.num_layers):
+            idx = m.tap(f"ridx.{l}", np.int32, B * T * K).reshape(B * T, K)
+            st = synth.routing_load(idx, E)
+            same = np.mean(np.sort(idx[:T], 1) == np.sort(route0[l], 1))
+            print(f"layer {l}: {st}; sequence 0 picks equal to the oracle's {same:.5f}")
+            assert st["touched"] == E
+            assert st["max_share"] <= 0.10
+            assert 0.43 <= st["top20_share"] <= 0.58
+            assert st["under_0p1pct"] <= 2
+            assert same >= 0.99
+    finally:
+        m.enable_taps(False)
+        be.dispose()
 
 
 def test_detect_spans_vs_oracle(small):

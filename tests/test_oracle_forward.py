@@ -124,3 +124,35 @@ def test_oracle_forward_all_ones_mask_is_elided(tiny):
     a = oracle.model_forward(PF_CONFIG, w, ids, mask=None, num_layers=L)
     b = oracle.model_forward(PF_CONFIG, w, ids, mask=np.ones(T, np.uint8), num_layers=L)
     assert np.array_equal(a, b)
+
+
+def test_synthetic_model_is_not_degenerate():
+    """The benchmark's synthetic model (synth.make_model_weights, "spread"
+    recipe, full size) on 512 tagged tokens through the oracle: the argmax
+    spreads over the classes and follows the ids' planted tags, the decoded
+    spans include multi-token runs, and routing reaches nearly every expert
+    with no expert above 10 % of the picks in any layer. The "uniform"
+    recipe (uniform nibbles 0..15 everywhere) collapses: from layer 1 on a
+    handful of experts take every pick and the argmax takes 1-3 classes."""
+    from parity_util import logit_spread, span_parity
+    from textsift_amd.spans import Chunk
+    T = 512
+    w = synth.make_model_weights(PF_CONFIG, seed=20260101)
+    ids = synth.tagged_token_ids(1000, T)
+    bits, route = oracle.model_forward(PF_CONFIG, w, ids, n_threads=8, return_routing=True)
+    lg = f16(bits)
+    classes, top = logit_spread(lg)
+    assert classes >= 30 and top <= 0.1
+    assert np.mean(np.argmax(lg, 1) == ids % PF_CONFIG.num_classes) >= 0.99
+    chunk = Chunk(ids, np.ones(T, np.uint8), list(range(0, 2 * T + 1, 2)), "ab" * T, 0, (0, T))
+    _, rep = span_parity(lg, lg, chunk)
+    assert rep["multi_token_spans"] >= 50
+    for l in range(PF_CONFIG.num_layers):
+        st = synth.routing_load(route[l], PF_CONFIG.num_experts)
+        assert st["touched"] >= 120 and st["max_share"] <= 0.10, (l, st)
+    del w
+    wu = synth.make_model_weights(PF_CONFIG, seed=20260101, num_layers=3, vocab_size=4096, recipe="uniform")
+    idu = synth.token_ids(1000, T, 4096)
+    bits, route = oracle.model_forward(PF_CONFIG, wu, idu, n_threads=8, num_layers=3, return_routing=True)
+    assert logit_spread(f16(bits))[0] <= 3
+    assert synth.routing_load(route[2], PF_CONFIG.num_experts)["touched"] <= 16

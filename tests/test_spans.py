@@ -264,3 +264,19 @@ def test_detect_long_input_equals_one_pass():
     assert len(one) > 50
     assert all(text[s.start:s.end] == s.text for s in got)
     assert sp.detect(text, be, tok, dec, max_chunk_tokens=10_000, min_confidence=1.0) == one
+
+
+def test_parity_util_lattice_matches_the_rules():
+    """The lattice parity_util scores paths with (for the span near-tie bound)
+    equals this file's tables, and the decoder's path is its optimum."""
+    from parity_util import SYNTH_OPERATING_POINT, path_score, transition_scores
+    rng = np.random.default_rng(5)
+    for cal in (sp.zero_calibration(), sp.load_calibration(SYNTH_OPERATING_POINT),
+                sp.ViterbiCalibration(*map(float, rng.normal(0, 1, 6)))):
+        t, start = transition_scores(cal)
+        t2, s2 = _tables(cal.biases())
+        assert np.array_equal(np.where(np.isinf(t), NEG, t).astype(np.float32), t2)
+        assert np.array_equal(np.where(np.isinf(start), NEG, start).astype(np.float32), s2)
+        lg = rng.normal(0, 2, (64, C)).astype(np.float32)
+        best = sp.ViterbiDecoder(cal).decode(lg)
+        assert abs(path_score(lg, best, cal) - _score(best, lg, t2, s2)) < 1e-3
