@@ -20,11 +20,14 @@
 //    8 values K = 32*lg + 8*j .. +7 from lane group lg. The activation
 //    operand uses the same permutation, so the dot product is unchanged.
 //  * Weights are repacked once (w4_repack): byte b of each dword holds k = b
-//    in its low nibble and k = b + 4 in its high nibble. Two masks (one
-//    shift) put the 8 values in bytes, and one v_perm_b32 per pair places two
-//    of them under 0x64 exponent bytes: (1024 + q) as packed fp16, in natural
-//    k order. One packed add subtracts (1024 + zp) exactly and one packed
-//    multiply applies the scale (the only rounding).
+//    in its low nibble and k = b + 4 in its high nibble. Two masks (no
+//    shift) isolate the low and the high nibbles in their bytes, and one
+//    v_perm_b32 per pair places two of them under exponent bytes: 0x64 for
+//    the low nibbles ((1024 + q) as packed fp16), 0x54 for the high ones
+//    ((64 + q): the nibble sits at mantissa bit 4, which weighs 1 at that
+//    exponent), in natural k order. One packed add subtracts (1024 + zp) or
+//    (64 + zp) exactly and one packed multiply applies the scale (the only
+//    rounding).
 //  * Activations are the shared operand: the workgroup's BT x 128 chunk is
 //    copied HBM -> LDS with global_load_lds_dwordx4 (no register staging),
 //    double buffered, in 256-byte rows whose 16-byte units are XOR-swizzled
@@ -56,18 +59,27 @@ __device__ __forceinline__ h4_t rope_entry(const _Float16* tb, int row, int pidx
 
 // One repacked dword (8 nibbles) -> fp16 (q - zp) * scale for k = 0..7.
 // off = (-(1024 + zp), -(1024 + zp)), sc = (scale, scale).
-__device__ __forceinline__ h8_t dequant_fold(uint32_t w, h2_t off, h2_t sc) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;          // k0 k1 k2 k3 (one per byte)
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // k4 k5 k6 k7
+// The low nibbles are masked into the low bits of each byte and placed under
+// 0x64 exponent bytes: fp16 1024 + q (mantissa ulp 1). The high nibbles are
+// masked in place (q << 4 in each byte, no shift) and placed under 0x54
+// exponent bytes: fp16 64 + q (exponent 21: mantissa bit 4 weighs 2^6 * 16 /
+// 1024 = 1). Their offset is -(64 + zp) = off + 960, exact like off. Both
+// subtractions and the scale multiply give exactly the values of the
+// single-magic form, with one shift fewer per dword.
+__device__ __forceinline__ h2_t off_high(h2_t off) { return off + h2_t{(_Float16)960.0f, (_Float16)960.0f}; }
+__device__ __forceinline__ h8_t dequant_fold(uint32_t w, h2_t off, h2_t off_hi, h2_t sc) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;          // k0 k1 k2 k3 (one per byte, bits 0-3)
+  const uint32_t hi = w & 0xF0F0F0F0u;          // k4 k5 k6 k7 (one per byte, bits 4-7)
   const uint32_t M = 0x64646464u;               // exponent bytes of 1024
-  const uint32_t p0 = __builtin_amdgcn_perm(M, lo, 0x04010400u);  // (1024 + k0, 1024 + k1)
+  const uint32_t MH = 0x54545454u;              // exponent bytes of 64
+  const uint32_t p0 = __builtin_amdgcn_perm(M, lo, 0x04010400u);   // (1024 + k0, 1024 + k1)
   const uint32_t p1 = __builtin_amdgcn_perm(M, lo, 0x04030402u);
-  const uint32_t p2 = __builtin_amdgcn_perm(M, hi, 0x04010400u);
-  const uint32_t p3 = __builtin_amdgcn_perm(M, hi, 0x04030402u);
+  const uint32_t p2 = __builtin_amdgcn_perm(MH, hi, 0x04010400u);  // (64 + k4, 64 + k5)
+  const uint32_t p3 = __builtin_amdgcn_perm(MH, hi, 0x04030402u);
   const h2_t d0 = (__builtin_bit_cast(h2_t, p0) + off) * sc;
   const h2_t d1 = (__builtin_bit_cast(h2_t, p1) + off) * sc;
-  const h2_t d2 = (__builtin_bit_cast(h2_t, p2) + off) * sc;
-  const h2_t d3 = (__builtin_bit_cast(h2_t, p3) + off) * sc;
+  const h2_t d2 = (__builtin_bit_cast(h2_t, p2) + off_hi) * sc;
+  const h2_t d3 = (__builtin_bit_cast(h2_t, p3) + off_hi) * sc;
   return __builtin_bit_cast(h8_t, u4_t{h2_bits(d0), h2_bits(d1), h2_bits(d2), h2_bits(d3)});
 }
 
@@ -107,7 +119,11 @@ struct StagedOut {
 // and weights are loaded at once, so a workgroup waits for memory once
 // instead of once per chunk (the latency that dominates when a GEMM is a few
 // workgroups).
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false>
+// EVENC (CT == 0 only): K / 128 is even. The chunk loop is unrolled by two
+// with the last chunk's register set fixed at compile time (a run-time choice
+// between the two sets made the 128-row tiles spill).
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false,
+          bool EVENC = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
@@ -250,11 +266,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
   auto compute = [&](int buf, const u4_t (&wr)[WF], const uint32_t (&szc)[WF]) {
-    h2_t off[WF], sc[WF];
+    h2_t off[WF], offh[WF], sc[WF];
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
       const h2_t pr = __builtin_bit_cast(h2_t, szc[f]);
       off[f] = h2_t{pr.x, pr.x};
+      offh[f] = off_high(off[f]);
       sc[f] = h2_t{pr.y, pr.y};
     }
     const _Float16* xb = xs_lds + buf * XS * PLANE;
@@ -262,7 +279,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
 #pragma unroll
-      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wr[f][j], off[f], sc[f]);
+      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
       const int unit = ((4 * lg + j) ^ l16) << 3;
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) {
@@ -359,25 +376,31 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       __syncthreads();
     }
   } else {
-    load_x(0, 0);
-    load_w(0, wraw, sz);
-    for (int c = 0; c + 1 < C; ++c) {
+    // chunk c's weights are in register set A (wraw, sz) for even c and B
+    // (wnext, sznext) for odd c, its activations in LDS buffer c & 1: the
+    // loop is unrolled by two so that neither the register sets nor the
+    // buffer addresses change at run time (no register copies per chunk)
+    auto step = [&](int c, int buf, const u4_t (&wc)[WF], const uint32_t (&scc)[WF], u4_t (&wn)[WF],
+                    uint32_t (&sn)[WF]) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      load_x(c + 1, (c & 1) ^ 1);
-      load_w(c + 1, wnext, sznext);
+      load_x(c + 1, buf ^ 1);
+      load_w(c + 1, wn, sn);
       // the expert GEMMs raise the wave's issue priority over the chunk's
       // MFMAs and dequantisation (and drop it for the loads and the barrier):
       // gate_up 235 -> 229 us, down -1 us; the dense QKV GEMM got slower with it
       if constexpr (GROUPED) __builtin_amdgcn_s_setprio(1);
-      compute(c & 1, wraw, sz);
+      compute(buf, wc, scc);
       if constexpr (GROUPED) __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-      for (int f = 0; f < WF; ++f) {
-        wraw[f] = wnext[f];
-        sz[f] = sznext[f];
-      }
+    };
+    load_x(0, 0);
+    load_w(0, wraw, sz);
+    int c = 0;
+    for (; c + 2 < C; c += 2) {
+      step(c, 0, wraw, sz, wnext, sznext);
+      step(c + 1, 1, wnext, sznext, wraw, sz);
     }
+    if constexpr (EVENC) step(c, 0, wraw, sz, wnext, sznext);  // the last chunk, C - 1, is then in set B
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
@@ -409,7 +432,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
     for (int c = 0; c < CT; ++c) compute(c, wall[c], szall[c]);
   } else {
-    compute((C - 1) & 1, wraw, sz);
+    if constexpr (EVENC) compute(1, wnext, sznext);
+    else compute(0, wraw, sz);
   }
   // the SwiGLU epilogue's clamp reads the accumulators with inline assembly
   if constexpr (EPI == Epi::SWIGLU_F16) {
@@ -671,11 +695,14 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
                               StagedOut<WF, BT, EPI, NW>::OK
                                   ? StagedOut<WF, BT, EPI, NW>::LDS + (EPI == Epi::F32_TOPK ? 128 * 4 : 0)
                                   : (size_t)0);
-  allow_lds(reinterpret_cast<const void*>(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>), lds);
-  ProfScope ps(b, name);
-  hipLaunchKernelGGL((k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM>), dim3((unsigned)grid), dim3(64 * NW), lds,
-                     b->stream, a);
-  PF_HIP(hipGetLastError());
+  auto go = [&](auto kern) {
+    allow_lds(reinterpret_cast<const void*>(kern), lds);
+    ProfScope ps(b, name);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), lds, b->stream, a);
+    PF_HIP(hipGetLastError());
+  };
+  if (CT == 0 && (a.K / KC) % 2 == 0) go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, CT == 0>);
+  else go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, false>);
 }
 
 template <int WF, int BT, int XS, bool GROUPED, int NW, int CT = 0>
@@ -959,11 +986,12 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   }
 
   auto compute = [&](int c) {
-    h2_t off[WF], sc[WF];
+    h2_t off[WF], offh[WF], sc[WF];
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
       const h2_t pr = __builtin_bit_cast(h2_t, sz[c][f]);
       off[f] = h2_t{pr.x, pr.x};
+      offh[f] = off_high(off[f]);
       sc[f] = h2_t{pr.y, pr.y};
     }
     const _Float16* xb = xs_lds + (c % NB) * PLANE;
@@ -971,7 +999,7 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
 #pragma unroll
-      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wraw[c][f][j], off[f], sc[f]);
+      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wraw[c][f][j], off[f], offh[f], sc[f]);
       const int unit = ((4 * lg + j) ^ l16) << 3;
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) {
