@@ -624,9 +624,13 @@ def bench_config(cfg_id, reps, variant="both", no_cpu=False, calib_mb=0):
                     b_.release()
                 pw += [w4, sz, buf(qw["bias"])]
             wsets.append(pw)
-        xb, rwb, rbb = buf(x), buf(rw_), buf(rb)
+        # the router weight is transposed to [E][D] once (as a weight upload would); the layer then
+        # runs the forward's fused router chain: 5 launches
+        xb, rws, rbb = buf(x), buf(rw_), buf(rb)
+        rwb = buf(nbytes=D * E * 2)
+        be.dispatch("transpose_f16", [rws, rwb], u32(D, E))
         ob, ib, wb = buf(nbytes=T * D * 2), buf(nbytes=T * K * 4), buf(nbytes=T * K * 4)
-        push = u32(T, D, E, K, F, 0, 0, 0)
+        push = u32(T, D, E, K, F, 0, 0, 1)
         name = "moe_ffn_w4"
         mk = lambda i: [xb, rwb, rbb] + wsets[i] + [ob, ib, wb]
         warm = time_dispatch(be, name, lambda i: mk(0), push, 1, reps) if do_warm else nan2

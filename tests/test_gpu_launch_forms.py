@@ -126,6 +126,67 @@ def test_moe_layer_fp16_vs_oracle(be, T, E, tile):
         assert counts[:8].sum() > 4 * counts[-8:].sum()
 
 
+@pytest.mark.parametrize("T", [2048, 700])
+def test_moe_layer_fused_router_chain(be, T):
+    """BASELINE config 3 through the chain the forward runs (moe_ffn_w4 with
+    the router weight transposed once by transpose_f16): the fp16-weight
+    router GEMM whose epilogue takes the top-4 and, above 1024 tokens,
+    counts each 64-row tile's picks per expert, the routing plan from those
+    counts (one kernel; below 1024 tokens the single-workgroup plan), the
+    grouped SwiGLU and down GEMMs and the combine. The routing equals the
+    oracle's top-4 (zig/wasm_exports.zig:367-426) on float64 logits of the
+    same fp16 inputs except where the 4th and 5th logits tie to within the
+    f32 accumulation error; the output is the oracle's expert-major dispatch
+    (browser/inference/expert.ts:104-212) of the GPU's routing to rel-err
+    < 2e-3; the routing weights are the softmax of the selected logits."""
+    cfg = PF_CONFIG
+    D, F, K, E = cfg.hidden_size, cfg.intermediate_size, cfg.num_experts_per_tok, cfg.num_experts
+    x = synth.to_fp16_bits(synth.normal(720 + T, T * D)).reshape(T, D)
+    rw_, rb = synth.zipf_router(721, D, E)
+    gu = synth.qweight(722, 2 * F, D, lead=(E,))
+    dn = synth.qweight(723, D, F, lead=(E,))
+    rwt = run(be, "transpose_f16", [rw_], [D * E * 2], u32s(D, E))[0].view(np.uint16).reshape(E, D)
+    assert np.array_equal(rwt, rw_.T)
+
+    def prep(qw, rows, kk):
+        w4, sz = run(be, "w4_prepare", [qw["int4"], qw["scales"], qw["zp"]], [E * rows * kk // 2,
+                                                                              E * rows * (kk // 32) * 4],
+                     u32s(E * rows, kk, 1, 0))
+        return [w4, sz, qw["bias"]]
+    ins = [x, rwt, rb] + prep(gu, 2 * F, D) + prep(dn, D, F)
+    out, ix, wt = run(be, "moe_ffn_w4", ins, [T * D * 2, T * K * 4, T * K * 4], u32s(T, D, E, K, F, 0, 0, 1))
+    y = out.view(np.uint16).reshape(T, D)
+    ridx = ix.view(np.int32).reshape(T, K)
+    rwts = wt.view(np.float32).reshape(T, K)
+    # routing vs float64 logits of the same fp16 inputs
+    lg = f16(x) @ f16(rw_) + f16(rb)
+    srt = -np.sort(-lg, axis=1)
+    tie = (srt[:, 3] - srt[:, 4]) < 1e-4 * (np.abs(srt[:, 3]) + 1.0)
+    want = np.argsort(-lg, axis=1, kind="stable")[:, :K]
+    same = np.all(np.sort(ridx, 1) == np.sort(want, 1), axis=1)
+    print(f"fused router chain T={T}: routing rows equal {same.mean():.5f}, near-tied rows {int(tie.sum())}")
+    assert np.all(same | tie)
+    sel = np.take_along_axis(lg, ridx.astype(np.int64), 1)
+    sm = np.exp(sel - sel.max(1, keepdims=True))
+    sm /= sm.sum(1, keepdims=True)
+    assert np.allclose(rwts, sm, rtol=0, atol=1e-5)
+    assert np.all(np.diff(np.take_along_axis(lg, ridx.astype(np.int64), 1)[~tie], axis=1) <= 1e-4)  # sorted
+    w = {}
+    for kk, vv in gu.items():
+        w[f"layers.0.experts.gate_up.{kk}"] = vv
+    for kk, vv in dn.items():
+        w[f"layers.0.experts.down.{kk}"] = vv
+    for name in ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.o_proj", "router"):
+        for kk, vv in synth.qweight(724, 64, 64).items():
+            w[f"layers.0.{name}.{kk}"] = vv
+    w["layers.0.input_layernorm"] = w["layers.0.post_attention_layernorm"] = np.zeros(D, np.uint16)
+    w["layers.0.attn.sinks"] = np.zeros(14, np.float32)
+    ref = oracle.expert_dispatch(cfg, w, 0, oracle.fp16_to_f32(x), ridx, rwts * np.float32(0.25), n_slices=8)
+    err = rel_err_norm(f16(y), f16(ref))
+    print(f"fused router chain T={T}: MoE output rel-err {err:.3e}")
+    assert err < 2e-3
+
+
 # ---------------------------------------------------------------- reference fixtures not run elsewhere
 
 def test_qmoe_gate_up_fixture(be, fixture):

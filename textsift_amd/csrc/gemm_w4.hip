@@ -36,6 +36,8 @@
 //  * The GEMM is computed transposed (D = W . X^T) as in gemm_int4.hip, so
 //    each lane ends with 4 consecutive output columns of one token and the
 //    RoPE / SwiGLU epilogues are lane-local.
+#include <type_traits>
+
 #include "common.h"
 #include "epilogue.h"
 #include "pfhip_internal.h"
@@ -122,9 +124,15 @@ struct StagedOut {
 // EVENC (CT == 0 only): K / 128 is even. The chunk loop is unrolled by two
 // with the last chunk's register set fixed at compile time (a run-time choice
 // between the two sets made the 128-row tiles spill).
+// W16: the weights are fp16 [N][K] (p.w16; no quantisation, no dequantisation):
+// BASELINE config 3's fp16 router.
+struct W16Reg {
+  u4_t v[4];
+};
 template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false,
-          bool EVENC = false>
+          bool EVENC = false, bool W16 = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
+  static_assert(!W16 || (CT == 0 && !GROUPED), "fp16 weights: dense large tiles only");
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
   constexpr int XI = BT / (4 * NW);  // 1 KB (4-row) direct loads per wave per plane per chunk
@@ -174,15 +182,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   // byte offsets, the chunk in the scalar offset: no address arithmetic per
   // load (rows past N read row N-1; never stored). The host checks that the
   // matrices' byte sizes fit the descriptors' 31-bit range.
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(p.w + (size_t)expert * p.w_gs), 0, p.N * kd * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wrs =
+      W16 ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.w16), 0, p.N * K * 2, 0x00020000)
+          : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w + (size_t)expert * p.w_gs), 0, p.N * kd * 4,
+                                              0x00020000);
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(p.wsz + (size_t)expert * p.wsz_gs), 0, p.N * nb * 4, 0x00020000);
   uint32_t woff[WF], soff[WF];
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
     const int n = min(n0 + (wave * WF + f) * 16 + l16, p.N - 1);
-    woff[f] = (uint32_t)(n * kd + lg * 4) * 4u;
+    woff[f] = W16 ? (uint32_t)(n * K + lg * 32) * 2u : (uint32_t)(n * kd + lg * 4) * 4u;
     soff[f] = (uint32_t)(n * nb + lg) * 4u;
   }
 
@@ -212,14 +222,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       }
   };
 
-  u4_t wraw[WF], wnext[WF];
+  using WR = std::conditional_t<W16, W16Reg, u4_t>;
+  WR wraw[WF], wnext[WF];
   uint32_t sz[WF], sznext[WF];
-  auto load_w = [&](int c, u4_t* wr, uint32_t* s) {
+  auto load_w = [&](int c, WR* wr, uint32_t* s) {
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
-      // chunk c: 128 values = 64 bytes of each row, and its 4 quant blocks' pairs
-      wr[f] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[f], c * 64, 0);
-      s[f] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff[f], c * 16, 0);
+      if constexpr (W16) {
+        // chunk c: this lane's 32 consecutive values (64 bytes), one 16-byte unit per MFMA step
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wr[f].v[j] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[f], c * 256 + j * 16, 0);
+        s[f] = 0u;
+      } else {
+        // chunk c: 128 values = 64 bytes of each row, and its 4 quant blocks' pairs
+        wr[f] = __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[f], c * 64, 0);
+        s[f] = __builtin_amdgcn_raw_buffer_load_b32(srs, soff[f], c * 16, 0);
+      }
     }
   };
 
@@ -265,7 +283,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
-  auto compute = [&](int buf, const u4_t (&wr)[WF], const uint32_t (&szc)[WF]) {
+  auto compute = [&](int buf, const WR (&wr)[WF], const uint32_t (&szc)[WF]) {
     h2_t off[WF], offh[WF], sc[WF];
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
@@ -279,7 +297,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
 #pragma unroll
-      for (int f = 0; f < WF; ++f) wd[f] = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
+      for (int f = 0; f < WF; ++f) {
+        if constexpr (W16) wd[f] = __builtin_bit_cast(h8_t, wr[f].v[j]);
+        else wd[f] = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
+      }
       const int unit = ((4 * lg + j) ^ l16) << 3;
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) {
@@ -380,7 +401,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     // (wnext, sznext) for odd c, its activations in LDS buffer c & 1: the
     // loop is unrolled by two so that neither the register sets nor the
     // buffer addresses change at run time (no register copies per chunk)
-    auto step = [&](int c, int buf, const u4_t (&wc)[WF], const uint32_t (&scc)[WF], u4_t (&wn)[WF],
+    auto step = [&](int c, int buf, const WR (&wc)[WF], const uint32_t (&scc)[WF], WR (&wn)[WF],
                     uint32_t (&sn)[WF]) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -678,7 +699,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 }
 
-template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false>
+template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false, bool W16 = false>
 void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   constexpr int BN = NW * WF * 16;
   const int n_tiles = (a.N + BN - 1) / BN;
@@ -701,15 +722,16 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), lds, b->stream, a);
     PF_HIP(hipGetLastError());
   };
-  if (CT == 0 && (a.K / KC) % 2 == 0) go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, CT == 0>);
-  else go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, false>);
+  if (CT == 0 && (a.K / KC) % 2 == 0) go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, CT == 0, W16>);
+  else go(&k_gemm_w4<WF, BT, XS, EPI, GROUPED, NW, CT, NORM, false, W16>);
 }
 
 template <int WF, int BT, int XS, bool GROUPED, int NW, int CT = 0>
 void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name) {
   // the small tile (CT > 0) is built with one fragment per wave for every
-  // epilogue and with two for the router's (N = 128 in one workgroup)
-  constexpr bool ALL = CT == 0 || WF == 1;
+  // epilogue and with two for the router's (N = 128 in one workgroup); the
+  // all-K 64-row expert tile (grouped, five fragments) for the expert GEMMs
+  constexpr bool ALL = CT == 0 || WF == 1 || (BT == 64 && WF == 5 && GROUPED);
   switch (epi) {
     case Epi::F16:
       if constexpr (ALL) return launch<WF, BT, XS, Epi::F16, GROUPED, NW, CT>(b, a, name);
@@ -723,8 +745,11 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
       if constexpr (ALL) return launch<WF, BT, XS, Epi::SWIGLU_F16, GROUPED, NW, CT>(b, a, name);
       break;
     case Epi::F32_TOPK:
-      if constexpr (WF == 2 && (BT == 128 || BT == 64 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4)
+      if constexpr (WF == 2 && (BT == 128 || BT == 64 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4) {
+        if constexpr (CT == 0 && (BT == 64 || BT == 128))
+          if (a.w16) return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT, false, true>(b, a, name);
         return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT>(b, a, name);
+      }
       break;
   }
   throw Error("gemm_w4: unsupported epilogue for this tile");
@@ -794,10 +819,14 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
              const char* prof_name) {
   PF_CHECK(a.K > 0 && a.K % KC == 0, "gemm_w4: K must be a positive multiple of 128");
   PF_CHECK(a.N > 0, "gemm_w4: N must be positive");
-  PF_CHECK(a.x && a.w && a.wsz && (a.out || epi == Epi::F32_TOPK), "gemm_w4: null operand");
+  PF_CHECK(a.x && ((a.w && a.wsz) || a.w16) && (a.out || epi == Epi::F32_TOPK), "gemm_w4: null operand");
+  if (a.w16)
+    PF_CHECK(epi == Epi::F32_TOPK && !grouped && (tile_t == 64 || tile_t == 128) && wf == 2 &&
+                 (reinterpret_cast<uintptr_t>(a.w16) & 15) == 0 && (long)a.N * a.K * 2 < (1L << 31),
+             "gemm_w4: fp16 weights are built for the router top-k tile (64 or 128 rows), 16-byte aligned");
   PF_CHECK(a.ldx % 8 == 0, "gemm_w4: activation row stride must allow 16-byte loads");
   PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
-           "gemm_w4: activations and weights must be 16-byte aligned");
+           "gemm_w4: activations and weights must be 16-byte aligned");  // (w is null with fp16 weights)
   // activation rows are addressed with 32-bit element offsets (grouped: a.M
   // slots bound every row the tile list or the row map can name)
   PF_CHECK((long)a.M * a.ldx < (1L << 31), "gemm_w4: activation offsets exceed 32 bits");
@@ -834,6 +863,11 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
              "gemm_w4: the top-k epilogue needs N == 128, K == 4, a 128- or 16-token tile of 128 columns and "
              "16-byte aligned f32 rows");
   if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
+  // 64-row expert tiles with K = 640 load all five chunks at once (80 KB of
+  // LDS, two workgroups per CU): a tile waits for memory once instead of
+  // once per chunk, which is what bounds these GEMMs at a few hundred tiles
+  if (tile_t == 64 && wf == 5 && grouped && a.K == 5 * KC)
+    return dispatch_epi<5, 64, 1, true, 4, 5>(b, g, epi, prof_name);
   if (tile_t == 64 && wf == 5) return dispatch_grouped<5, 64>(b, g, epi, grouped, prof_name);
   if (tile_t == 128 && wf == 2) return dispatch_grouped<2, 128>(b, g, epi, grouped, prof_name);
   if (tile_t == 64 && wf == 2) return dispatch_grouped<2, 64>(b, g, epi, grouped, prof_name);

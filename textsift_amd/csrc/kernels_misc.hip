@@ -1423,6 +1423,14 @@ void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, cons
                             eps);
 }
 
+void transpose_f16(pfhip_backend* b, const uint16_t* src, uint16_t* dst, int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return;
+  ProfScope ps(b, "transpose_f16");
+  hipLaunchKernelGGL(k_transpose_f16, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, b->stream, src, dst,
+                     rows, cols);
+  PF_HIP(hipGetLastError());
+}
+
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
                  int D, int E, uint16_t* wt) {
   PF_CHECK(D > 0 && D % 32 == 0 && E > 0, "router_f16w: D must be a positive multiple of 32");

@@ -108,6 +108,8 @@ struct GemmArgs {
   // gemm_w4 only: repacked weights in w, and per block (fp16 -(1024+zp), fp16 scale)
   const uint32_t* wsz = nullptr;  // [N][K/32]
   size_t wsz_gs = 0;
+  // gemm_w4, router top-k tile only: fp16 weights [N][K] instead of w / wsz
+  const uint16_t* w16 = nullptr;
   void* out = nullptr;
   uint16_t* out_lo = nullptr;    // SWIGLU_SPLIT: lo plane of the output
   int ldo = 0;
@@ -233,6 +235,8 @@ void moe_combine_norm(pfhip_backend* b, const int32_t* idx, const float* w, cons
                       bool y16, const uint16_t* residual, uint16_t* h_out, const uint16_t* gamma, uint16_t* norm_hi,
                       uint16_t* norm_lo, int T, int K, int D, float eps);
 // fp16-weight router GEMM (MFMA); wt: scratch for W^T, E * D fp16, 16-byte aligned.
+// [rows][cols] fp16 -> [cols][rows]
+void transpose_f16(pfhip_backend* b, const uint16_t* src, uint16_t* dst, int rows, int cols);
 void router_f16w(pfhip_backend* b, const uint16_t* x, const uint16_t* w, const uint16_t* bias, float* logits, int T,
                  int D, int E, uint16_t* wt);
 

@@ -172,14 +172,21 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
 }
 
 // The MoE FFN layer of BASELINE config 3 in the forward's fp16 numerics, on
-// weights already in the gemm_w4 form (w4_prepare): fp16 router W [D][E]
-// (+ bias) -> router_topk -> routing plan -> gate_up grouped GEMM + SwiGLU
-// (fp16 out) -> down grouped GEMM (f32 out) -> combine into fp16 out.
-// Expert tiles as the forward chooses them (expert_tile).
+// weights already in the gemm_w4 form (w4_prepare): fp16 router (+ bias) ->
+// top-4 + softmax -> routing plan -> gate_up grouped GEMM + SwiGLU (fp16
+// out) -> down grouped GEMM (fp16 out) -> combine into fp16 out. Expert
+// tiles as the forward chooses them (expert_tile).
+// router_t: the router weight transposed once beforehand ([E][D], the
+// transpose_f16 dispatch), for 128 experts and top-4: the chain the forward
+// runs -- one router GEMM whose epilogue selects the experts and counts each
+// 64-row tile's picks per expert, then one kernel for the plan (above 1024
+// tokens; below, the single-workgroup plan kernel): five launches in all.
+// Otherwise (router W [D][E]): transpose, router GEMM, top-k, plan, then the
+// same expert kernels.
 static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw, const uint16_t* rb,
                          const uint32_t* guw, const uint32_t* gus, const uint16_t* gub, const uint32_t* dnw,
                          const uint32_t* dns, const uint16_t* dnb, uint16_t* out, int32_t* ridx, float* rwt, int T,
-                         int D, int E, int K, int F, ExpertTile et) {
+                         int D, int E, int K, int F, ExpertTile et, bool router_t) {
   if (et.t == 0) et = expert_tile(T, K, E, true, D, F);
   const size_t S = (size_t)T * K;
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
@@ -191,9 +198,22 @@ static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw
   uint16_t* glu = reinterpret_cast<uint16_t*>(s); s += al(S * F * 2);
   float* y = reinterpret_cast<float*>(s); s += al(S * D * 4);
   MoePlan m = moe_plan_carve(s, T, K, E, et.t);
-  router_f16w(b, x, rw, rb, logits, T, D, E, wt);
-  router_topk(b, logits, ridx, rwt, T, E, K, 1.0f);
-  moe_route(b, ridx, T, K, E, m);
+  if (router_t) {
+    PF_CHECK(E == 128 && K == 4 && D % 128 == 0, "moe_ffn_w4: the transposed router is built for 128 experts, top-4");
+    constexpr int RT = 64;  // router rows per tile (divides the plan's 1024-token blocks)
+    GemmArgs r;
+    r.x = x; r.ldx = D; r.w16 = rw; r.bias = rb;
+    r.out = nullptr; r.ldo = E; r.M = T; r.N = E; r.K = D;
+    r.topk_idx = ridx; r.topk_w = rwt; r.topk_k = K; r.topk_wscale = 1.0f;
+    if (T > 1024) r.topk_counts = m.tile_counts;
+    gemm_w4(b, r, XKind::F16, Epi::F32_TOPK, false, RT, 2, "moe_router");
+    if (T > 1024) moe_route_counts(b, ridx, m.tile_counts, RT, T, K, E, m);
+    else moe_route(b, ridx, T, K, E, m);
+  } else {
+    router_f16w(b, x, rw, rb, logits, T, D, E, wt);
+    router_topk(b, logits, ridx, rwt, T, E, K, 1.0f);
+    moe_route(b, ridx, T, K, E, m);
+  }
   GemmArgs g;
   g.x = x; g.ldx = D; g.row_map = m.slot_token;
   g.w = reinterpret_cast<const uint8_t*>(guw); g.wsz = gus; g.wsz_gs = (size_t)2 * F * (D / 32);
@@ -476,6 +496,15 @@ static std::vector<KernelEntry>& registry() {
                  w4_prepare(b, bp<uint8_t>(bs, 0), bp<uint16_t>(bs, 1), zp ? bp<uint8_t>(bs, 2) : nullptr,
                             bp<uint32_t>(bs, 3), bp<uint32_t>(bs, 4), rows, K);
                }});
+  // transpose_f16: [rows][cols] fp16 -> [cols][rows] (a weight's layout, prepared once).
+  // push {rows, cols}; bindings [src, dst]
+  r.push_back({"transpose_f16", 2, 8, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                 const int rows = (int)pu(p, 0), cols = (int)pu(p, 1);
+                 PF_CHECK(rows > 0 && cols > 0, "transpose_f16: bad shape");
+                 need(bs, 0, (size_t)rows * cols * 2, "transpose_f16");
+                 need(bs, 1, (size_t)rows * cols * 2, "transpose_f16");
+                 transpose_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), rows, cols);
+               }});
   // matmul_w4: the fp16 forward's GEMM on prepared weights (w4_prepare output).
   // push {T, N, K, out_f32, tile_t (0: the forward's choice for T rows), wf};
   // bindings [x fp16 [T][K], w4, sz, bias fp16 [N], out [T][N]]
@@ -495,10 +524,11 @@ static std::vector<KernelEntry>& registry() {
                  matmul_w4_auto(b, a, out_f32 ? Epi::F32 : Epi::F16, (int)pu(p, 4), (int)pu(p, 5), "matmul_w4");
                }});
   // moe_ffn_w4: moe_ffn in the fp16 numerics on prepared expert weights (BASELINE config 3 as the
-  // forward runs it). push {T, D, E, K, dff, tile_t, wf, 0} (tile_t 0: the forward's expert tile;
-  // else one of gemm_w4's grouped tiles: (128, 4), (64, 5), (64, 1), (16, 1)); bindings [x fp16 [T][D], router_w fp16 [D][E],
-  // router_bias fp16 [E], gu.w4, gu.sz, gu.bias, dn.w4, dn.sz, dn.bias, out fp16 [T][D], routing_idx [T][K],
-  // routing_w [T][K]]
+  // forward runs it). push {T, D, E, K, dff, tile_t, wf, router_t} (tile_t 0: the forward's expert tile;
+  // else one of gemm_w4's grouped tiles: (128, 4), (64, 5), (64, 1), (16, 1); router_t 1: router_w is
+  // transposed, [E][D] (transpose_f16), and E == 128, K == 4: the forward's fused router chain);
+  // bindings [x fp16 [T][D], router_w fp16 [D][E] (or [E][D]), router_bias fp16 [E], gu.w4, gu.sz, gu.bias,
+  // dn.w4, dn.sz, dn.bias, out fp16 [T][D], routing_idx [T][K], routing_w [T][K]]
   r.push_back({"moe_ffn_w4", 12, 32, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  const int T = (int)pu(p, 0), D = (int)pu(p, 1), E = (int)pu(p, 2), K = (int)pu(p, 3);
                  const int F = (int)pu(p, 4);
@@ -519,7 +549,7 @@ static std::vector<KernelEntry>& registry() {
                  moe_ffn_fp16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<uint16_t>(bs, 2), bp<uint32_t>(bs, 3),
                               bp<uint32_t>(bs, 4), bp<uint16_t>(bs, 5), bp<uint32_t>(bs, 6), bp<uint32_t>(bs, 7),
                               bp<uint16_t>(bs, 8), bp<uint16_t>(bs, 9), bp<int32_t>(bs, 10), bp<float>(bs, 11), T, D, E,
-                              K, F, ExpertTile{(int)pu(p, 5), (int)pu(p, 6)});
+                              K, F, ExpertTile{(int)pu(p, 5), (int)pu(p, 6)}, pu(p, 7) != 0);
                }});
   // moe_route: push {T, K, E, tile_t}; bindings [routing_idx, expert_off, slot_token, slot_of, tiles, num_tiles]
   r.push_back({"moe_route", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
