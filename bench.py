@@ -805,6 +805,9 @@ def main():
     ap.add_argument("--latency", action="store_true",
                     help="single-sequence forward latency at the token counts the reference publishes, then exit")
     args = ap.parse_args()
+    if args.copy_calibration_mb:
+        # the counter calibration's copy and gather kernels are measurement tooling of the library
+        os.environ["PFHIP_TOOLING"] = "1"
 
     if args.blas_torch:  # the torch half of --blas-reference, in a process of its own
         from textsift_amd.config import PF_CONFIG

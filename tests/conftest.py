@@ -10,6 +10,10 @@ if ROOT not in sys.path:
 
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
+# the library's measurement and probe kernels (probe_fast_math, probe_mfma_f16,
+# copy16, ...) are registered only with this set
+os.environ.setdefault("PFHIP_TOOLING", "1")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")

@@ -141,6 +141,63 @@ __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x
   }
 }
 
+// rms_norm with fp16 output for D = 128 NU: one wave takes 4 rows as 4 D / 8
+// = 64 NU 16-byte units, NU per lane (unit u = 64 i + lane of the wave's
+// rows; row u / (D / 8)), so every load and store instruction of the wave
+// moves 1 KB with all lanes active (the 8-byte, one-row-per-wave form moved
+// 512 B, the last instruction of a 640-wide row half empty). Each lane keeps
+// a partial sum of squares per row; the 4 row sums are wave reductions.
+template <int NU>
+__global__ __launch_bounds__(256) void k_rms_norm4(const uint16_t* __restrict__ x, const uint16_t* __restrict__ g,
+                                                   uint16_t* __restrict__ out, int T, float eps) {
+  constexpr int D = 128 * NU, UPR = D / 8;
+  const int lane = threadIdx.x & 63;
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+  if (t0 >= T) return;
+  u4_t raw[NU];
+  int row[NU], col[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = 64 * i + lane;
+    row[i] = u / UPR;
+    col[i] = (u - row[i] * UPR) * 8;
+    const int t = min(t0 + row[i], T - 1);
+    raw[i] = *reinterpret_cast<const u4_t*>(x + (size_t)t * D + col[i]);
+  }
+  float v[NU][8];
+  float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    h4_to_f(u2_t{raw[i].x, raw[i].y}, v[i]);
+    h4_to_f(u2_t{raw[i].z, raw[i].w}, v[i] + 4);
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s += v[i][r] * v[i][r];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ss[r] += row[i] == r ? s : 0.0f;
+  }
+  float inv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) inv[r] = 1.0f / sqrtf(wave_sum(ss[r]) * (1.0f / (float)D) + eps);
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int t = t0 + row[i];
+    const float ir = row[i] == 0 ? inv[0] : row[i] == 1 ? inv[1] : row[i] == 2 ? inv[2] : inv[3];
+    const u4_t gw = *reinterpret_cast<const u4_t*>(g + col[i]);
+    float gm[8], y[8];
+    h4_to_f(u2_t{gw.x, gw.y}, gm);
+    h4_to_f(u2_t{gw.z, gw.w}, gm + 4);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = v[i][r] * ir * gm[r];
+    // (the zero-tolerant fast test: the embedding rows this norm follows hold
+    // exact zeros wherever q == zp, which the plain test sends to the exact
+    // software path -- two fifths of the units of the forward's synthetic
+    // model, most of this kernel's time)
+    const u2_t lo = to_f16x4_z(y), hi = to_f16x4_z(y + 4);
+    if (t < T) *reinterpret_cast<u4_t*>(out + (size_t)t * D + col[i]) = u4_t{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
 // add_rmsnorm_fp16_to_f32 (:288-350): sum = a + b (fp16 store), sumsq of the
 // unrounded f32 sum, normalise the rounded sum.
 template <int MODE>
@@ -1209,7 +1266,13 @@ void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16
   PF_CHECK(D > 0 && D % 4 == 0 && D <= 256 * MAXJ, "rms_norm: D must be a multiple of 4, at most 1024");
   if (T <= 0) return;
   ProfScope ps(b, "rms_norm");
-  hipLaunchKernelGGL(k_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
+  const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(g) |
+                      reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const dim3 g16((T + 15) / 16);  // 4 waves x 4 rows per block
+  if (al16 && D == 640) hipLaunchKernelGGL(k_rms_norm4<5>, g16, dim3(256), 0, b->stream, x, g, out, T, eps);
+  else if (al16 && D == 512) hipLaunchKernelGGL(k_rms_norm4<4>, g16, dim3(256), 0, b->stream, x, g, out, T, eps);
+  else if (al16 && D == 768) hipLaunchKernelGGL(k_rms_norm4<6>, g16, dim3(256), 0, b->stream, x, g, out, T, eps);
+  else hipLaunchKernelGGL(k_rms_norm<OUT_F16>, dim3((T + 3) / 4), dim3(256), 0, b->stream, x, g, out, nullptr, T, D, eps);
   PF_HIP(hipGetLastError());
 }
 

@@ -6,6 +6,7 @@
 // validate binding counts and push-block sizes before launching
 // (native/vulkan_backend.zig:246-248, 288-290).
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <mutex>
@@ -381,34 +382,6 @@ static std::vector<KernelEntry>& registry() {
   r.push_back({"matmul_int4_fp16_f32", 6, 16, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
                  run_matmul(b, bs, p, false, true, "matmul_int4_fp16_f32");
                }});
-  // copy16: bindings [src, dst], push {bytes} (a plain copy of known size)
-  r.push_back({"copy16", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
-                 const size_t n = pu(p, 0);
-                 need(bs, 0, n, "copy16");
-                 need(bs, 1, n, "copy16");
-                 copy16(b, bs[0]->ptr, bs[1]->ptr, n);
-               }});
-  // copy16_lds: bindings [src, dst], push {bytes}; the copy with HBM -> LDS loads
-  r.push_back({"copy16_lds", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
-                 const size_t n = pu(p, 0);
-                 need(bs, 0, n, "copy16_lds");
-                 need(bs, 1, n, "copy16_lds");
-                 copy16_lds(b, bs[0]->ptr, bs[1]->ptr, n);
-               }});
-  // gather16: bindings [table, idx i32 [n], dst [n][16 B]], push {n, table_units}
-  r.push_back({"gather16", 3, 8, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
-                 const size_t n = pu(p, 0);
-                 const uint32_t tu = pu(p, 1);
-                 need(bs, 0, (size_t)tu * 16, "gather16");
-                 need(bs, 1, n * 4, "gather16");
-                 need(bs, 2, n * 16, "gather16");
-                 gather16(b, bs[0]->ptr, tu, bp<int32_t>(bs, 1), bs[2]->ptr, n);
-               }});
-  // probe_fast_math: push {which, lo, hi}; binding [out u32 x3]
-  r.push_back({"probe_fast_math", 1, 12, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
-                 need(bs, 0, 12, "probe_fast_math");
-                 probe_fast_math(b, (int)pu(p, 0), pu(p, 1), pu(p, 2), bp<uint32_t>(bs, 0));
-               }});
   // matmul_int4_w4: the scale-folded GEMM of the fp16 forward path (gemm_w4).
   // push {T, N, K, out_f32, tile_t, wf}; bindings [x fp16, w, scales, zp, bias, out]
   r.push_back({"matmul_int4_w4", 6, 24, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
@@ -702,12 +675,49 @@ static std::vector<KernelEntry>& registry() {
                  moe_combine(b, bp<int32_t>(bs, 14), bp<float>(bs, 15), m.slot_of, y, f16, nullptr, nullptr,
                              bp<uint16_t>(bs, 13), T, K, D);
                }});
-  r.push_back({"probe_mfma_f16", 3, 0, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*) {
-                 need(bs, 0, 16 * 32 * 2, "probe_mfma_f16");
-                 need(bs, 1, 32 * 16 * 2, "probe_mfma_f16");
-                 need(bs, 2, 16 * 16 * 4, "probe_mfma_f16");
-                 probe_mfma_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<float>(bs, 2));
-               }});
+  // Measurement and test tooling, registered only when PFHIP_TOOLING=1 is in
+  // the environment at the first dispatch (the test suite and the bench's
+  // counter calibration set it): copies and a gather of known size (the HBM
+  // counters' bytes-per-byte factors) and probes of the hardware's MFMA
+  // operand layout and fast-math instructions. None is used by the forward
+  // or the reference's kernel surface.
+  const char* tool = getenv("PFHIP_TOOLING");
+  if (tool && !strcmp(tool, "1")) {
+    // copy16: bindings [src, dst], push {bytes} (a plain copy of known size)
+    r.push_back({"copy16", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                   const size_t n = pu(p, 0);
+                   need(bs, 0, n, "copy16");
+                   need(bs, 1, n, "copy16");
+                   copy16(b, bs[0]->ptr, bs[1]->ptr, n);
+                 }});
+    // copy16_lds: bindings [src, dst], push {bytes}; the copy with HBM -> LDS loads
+    r.push_back({"copy16_lds", 2, 4, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                   const size_t n = pu(p, 0);
+                   need(bs, 0, n, "copy16_lds");
+                   need(bs, 1, n, "copy16_lds");
+                   copy16_lds(b, bs[0]->ptr, bs[1]->ptr, n);
+                 }});
+    // gather16: bindings [table, idx i32 [n], dst [n][16 B]], push {n, table_units}
+    r.push_back({"gather16", 3, 8, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                   const size_t n = pu(p, 0);
+                   const uint32_t tu = pu(p, 1);
+                   need(bs, 0, (size_t)tu * 16, "gather16");
+                   need(bs, 1, n * 4, "gather16");
+                   need(bs, 2, n * 16, "gather16");
+                   gather16(b, bs[0]->ptr, tu, bp<int32_t>(bs, 1), bs[2]->ptr, n);
+                 }});
+    // probe_fast_math: push {which, lo, hi}; binding [out u32 x3]
+    r.push_back({"probe_fast_math", 1, 12, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t* p) {
+                   need(bs, 0, 12, "probe_fast_math");
+                   probe_fast_math(b, (int)pu(p, 0), pu(p, 1), pu(p, 2), bp<uint32_t>(bs, 0));
+                 }});
+    r.push_back({"probe_mfma_f16", 3, 0, [](pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*) {
+                   need(bs, 0, 16 * 32 * 2, "probe_mfma_f16");
+                   need(bs, 1, 32 * 16 * 2, "probe_mfma_f16");
+                   need(bs, 2, 16 * 16 * 4, "probe_mfma_f16");
+                   probe_mfma_f16(b, bp<uint16_t>(bs, 0), bp<uint16_t>(bs, 1), bp<float>(bs, 2));
+                 }});
+  }
   return r;
 }
 

@@ -150,8 +150,9 @@ ROUTER_SKEW = 0.28
 # token whose 4th and 5th router logits nearly tie may take either expert
 # (both are correct to the inputs' precision); the MoE output's size sets
 # how far such a token's logits move (measured on the GPU at 16 x 2048:
-# logit rel-err vs the oracle 2.0e-3 with the down projection at 1/16 and
-# router scales at 1x, 0.8e-3 as chosen here).
+# logit rel-err vs the CPU restatement of the WASM path 2.0e-3 with the
+# down projection at 1/16 and the router scales at 1x, 0.8e-3 as chosen
+# here).
 EMBED_SCALE = (0.08, 0.32)
 OUT_PROJ_SCALE = (0.0003125, 0.00125)
 OUT_PROJ_BIAS_SIGMA = 0.00125
