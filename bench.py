@@ -48,11 +48,11 @@ KERNEL_LABELS = [
     ("gemm_qkv_rope", ("k_gemm_w4<", "(pf::Epi)2, false")),
     ("gemm_o_add_rmsnorm", ("k_gemm_w4_rownorm",)),
     ("gemm_o", ("k_gemm_w4<4, 128", "(pf::Epi)0, false")),
-    ("gemm_o", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 7>")),      # all-K small tile, K = 896
+    ("gemm_o", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 7,")),      # all-K small tile, K = 896
     ("gemm_router", ("k_gemm_w4<2, ", "(pf::Epi)5, false")),
     ("gemm_router", ("k_gemm_w4<2, ", "(pf::Epi)1, false")),
     ("gemm_classifier", ("k_gemm_w4<1, 64", "(pf::Epi)0, false")),
-    ("gemm_classifier", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 5>")),  # all-K small tile, K = 640
+    ("gemm_classifier", ("k_gemm_w4<1, 16", "(pf::Epi)0, false, 4, 5,")),  # all-K small tile, K = 640
     ("banded_attention", ("k_banded_attention",)),
     ("moe_combine_norm", ("k_moe_combine",)),
     ("add_rmsnorm_f16", ("k_add_rms_norm",)),
@@ -232,8 +232,12 @@ def stats_report(stats_csv, top=20):
     return "\n".join(lines)
 
 
-def read_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed traffic summary, or None."""
+def read_traffic(kernel, B, T):
+    """HBM bytes per launch of `kernel` from the committed traffic summary, or
+    None. The summary is of the 16 x 2048 headline forward, so other shapes get
+    None."""
+    if (B, T) != (16, 2048):
+        return None
     path = os.path.join(ROOT, "profiles", "forward_16x2048_hbm_traffic.md")
     if not os.path.exists(path):
         return None
@@ -926,7 +930,7 @@ def main():
         avg_s = ms / n / 1000.0
         achieved = flops[dom] / avg_s / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_FP16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": read_traffic(dom),
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP16_PEAK_TFLOPS, 4), "traffic": read_traffic(dom, B, T),
                 "flops_per_launch": flops[dom], "avg_launch_us": round(avg_s * 1e6, 2),
                 "launches_timed": n}
     total_flops = sum(flops[k] * cfg.num_layers for k in
