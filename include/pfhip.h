@@ -170,6 +170,17 @@ int pfhip_model_read_tap(pfhip_model* m, const char* name, void* dst, size_t n, 
  * host). Names: "qkv.L", "att.L", "h2.L", "router.L", "ridx.L", "rw.L",
  * "h.L" for layer L, and "logits16". */
 int pfhip_model_enable_taps(pfhip_model* m, int on);
+/* HIP graphs for pfhip_model_forward_device / pfhip_model_forward (on by
+ * default). The reference records a forward's whole dispatch sequence into
+ * one command encoder and submits it once (native/backend.ts:485,693); here
+ * the first call for a (batch, seq_len, ids, mask, logits) combination runs
+ * eagerly, the second captures its launches into a HIP graph and every later
+ * one replays it (16 combinations are kept, the oldest dropped first). Buffer
+ * contents may change between calls; the buffers themselves are part of the
+ * key. Forwards with taps or profiling enabled always run eagerly, and the
+ * graphs are dropped whenever weights are set, the model is finalized, or the
+ * scratch or RoPE tables grow. on = 0 drops them and runs eagerly. */
+int pfhip_model_enable_graphs(pfhip_model* m, int on);
 
 /* The YARN RoPE tables the forward uses for sequence length T
  * (browser/inference/rope.ts:27-144): fp16 bits [T][head_dim/2] each. */

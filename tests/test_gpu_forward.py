@@ -190,6 +190,33 @@ def test_full_model_forward_vs_oracle(full_ref, precision):
     _check_logits(got, ref, f"full model T={T} precision={precision}")
 
 
+def test_full_model_small_t_vs_oracle(full_ref):
+    """The full-size model at the reference's published small token counts
+    (T = 7, 16: the router's single 16-row workgroup also builds the routing
+    plan; T = 25, 80: the separate plan kernel), batch 1 and 2, against the
+    oracle's forward of the same ids: rel-err < 2e-3 and every argmax equal.
+    Each shape runs three times (eager, captured, replayed)."""
+    w = full_ref[0]
+    be = HipBackend(w)
+    be.warmup()
+    try:
+        for B, T in ((1, 7), (1, 16), (2, 8), (1, 25), (1, 80)):
+            ids = synth.tagged_token_ids(300 + T, B * T).reshape(B, T)
+            ref = np.concatenate([oracle.model_forward(PF_CONFIG, w, ids[b]).view(np.float16).astype(np.float32)
+                                  .reshape(T, -1) for b in range(B)])
+            for rep in range(3):
+                got = be.forward_batch(ids).reshape(B * T, -1) if B > 1 else \
+                    be.forward(ids[0], np.ones(T, np.uint8)).as_matrix()
+                err = rel_err_norm(got, ref)
+                agree = np.mean(np.argmax(got, 1) == np.argmax(ref, 1))
+                if rep == 0:
+                    print(f"full model B={B} T={T}: rel-err {err:.3e}, argmax agreement {agree:.4f}")
+                assert err < 2e-3
+                assert agree == 1.0
+    finally:
+        be.dispose()
+
+
 @pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
 def test_full_batch_16x2048(full_ref, precision):
     """The benchmarked launch set (BASELINE config 5 at its stated batch):
@@ -553,3 +580,44 @@ def test_o_residual_norm_vs_oracle(small, B, T):
     # the scale-folded fp16 weights move o by ~2^-12 relative, which changes
     # the fp16 rounding of about a fifth of the sums
     assert np.mean(h2 == s_ref) > 0.6
+
+
+@pytest.mark.parametrize("T,masked", [(7, False), (80, True), (300, False)])
+def test_forward_graph_replay_matches_eager(small, T, masked):
+    """The device-resident forward replays a captured HIP graph from its
+    second call per (batch, seq_len, buffers). Every replay, with new token
+    ids written into the same buffers and eager work of another shape between
+    replays, gives the logits of the eager forward bit for bit."""
+    w, be = small
+    m, dev = be.model, be.device
+    C = PF_CONFIG.num_classes
+    rng = np.random.default_rng(T)
+    reps = 5
+    ids_all = [rng.integers(0, V, T).astype(np.int32) for _ in range(reps)]
+    mask_all = [(rng.random(T) < 0.8).astype(np.uint8) if masked else None for _ in range(reps)]
+    ids_buf = dev.buffer(nbytes=T * 4)
+    mask_buf = dev.buffer(nbytes=T) if masked else None
+    out = dev.buffer(nbytes=T * C * 4)
+    try:
+        m.enable_graphs(False)
+        want = []
+        for ids, mask in zip(ids_all, mask_all):
+            ids_buf.write(ids)
+            if masked:
+                mask_buf.write(mask)
+            m.forward_device(ids_buf, mask_buf, 1, T, out)
+            want.append(out.read(np.float32))
+        m.enable_graphs(True)
+        for rep, (ids, mask) in enumerate(zip(ids_all, mask_all)):
+            ids_buf.write(ids)
+            if masked:
+                mask_buf.write(mask)
+            m.forward_device(ids_buf, mask_buf, 1, T, out)  # rep 0 eager, rep 1 captured, then replays
+            got = out.read(np.float32)
+            assert np.array_equal(got.view(np.uint32), want[rep].view(np.uint32)), f"call {rep} differs from eager"
+            be.forward(rng.integers(0, V, 33).astype(np.int32), np.ones(33, np.uint8))  # other work in between
+    finally:
+        m.enable_graphs(True)
+        for b in (ids_buf, mask_buf, out):
+            if b is not None:
+                b.release()

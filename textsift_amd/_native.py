@@ -80,6 +80,7 @@ EXPORTS = [
                                                      C.c_void_p, C.c_char_p, C.c_size_t]),
     ("pfhip_model_read_tap", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
     ("pfhip_model_enable_taps", C.c_int, [C.c_void_p, C.c_int]),
+    ("pfhip_model_enable_graphs", C.c_int, [C.c_void_p, C.c_int]),
     ("pfhip_rope_tables", C.c_int, [C.POINTER(ModelConfigC), C.c_uint32, C.c_void_p, C.c_void_p]),
     ("pfhip_profile_enable", C.c_int, [C.c_void_p, C.c_int]),
     ("pfhip_profile_select", C.c_int, [C.c_void_p, C.c_char_p]),
@@ -260,6 +261,11 @@ class Model:
 
     def enable_taps(self, on: bool = True):
         lib().pfhip_model_enable_taps(self.handle, int(on))
+
+    def enable_graphs(self, on: bool = True):
+        """pfhip_model_enable_graphs: replay each (batch, seq_len, buffers)
+        forward from a HIP graph after its first call (default on)."""
+        lib().pfhip_model_enable_graphs(self.handle, int(on))
 
     def tap(self, name: str, dtype, count: int) -> np.ndarray:
         out = np.empty(count, np.dtype(dtype))

@@ -89,6 +89,19 @@ void copy_sync(pfhip_backend* b, void* dst, const void* src, size_t n, hipMemcpy
 
 }  // namespace
 
+// One captured forward: the launches of run_forward for one (batch,
+// seq_len) on fixed ids / mask / logits buffers, the model's scratch and RoPE
+// tables. An entry without exec has run once eagerly: the first call of a
+// shape grows the scratch and tables and sets the kernels' attributes, none
+// of which a capture may contain; the second is captured and replayed.
+struct FwdGraph {
+  int B = 0, T = 0;
+  const void* ids = nullptr;
+  const void* mask = nullptr;
+  void* logits = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
 struct pfhip_model {
   pfhip_backend* b = nullptr;
   pfhip_model_config cfg{};
@@ -114,6 +127,11 @@ struct pfhip_model {
   bool taps = false;
   bool in_noalloc = false;
   std::map<std::string, std::vector<uint8_t>> tap;
+  // HIP graphs of the device-resident forward, one per (batch, seq_len,
+  // buffers): the reference records a forward's whole dispatch sequence into
+  // one encoder and submits it once (native/backend.ts:485,693)
+  bool graphs = true;
+  std::vector<FwdGraph> graph_cache;
 };
 
 namespace {
@@ -306,11 +324,20 @@ static void record_tap(pfhip_model* m, const std::string& name, const void* dev,
   PF_HIP(hipStreamSynchronize(m->b->stream));
 }
 
+// Drops every captured forward (their launches name the scratch, tables
+// and weights of the moment they were captured).
+static void clear_graphs(pfhip_model* m) {
+  for (auto& g : m->graph_cache)
+    if (g.exec) hipGraphExecDestroy(g.exec);
+  m->graph_cache.clear();
+}
+
 // Host-built YARN tables for T positions, replacing smaller ones.
 static void ensure_rope(pfhip_model* m, int T) {
   pfhip_backend* b = m->b;
   std::vector<uint16_t> cs, sn;
   build_rope_tables(m->cfg, T, cs, sn);
+  clear_graphs(m);
   if (m->rope_cos) {
     PF_HIP(hipStreamSynchronize(b->stream));
     hipFree(m->rope_cos);
@@ -359,6 +386,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
                                                  std::to_string(NOALLOC_SCRATCH_BYTES) +
                                                  " of the allocation-free forward");
   } else if (bytes > m->scratch_bytes) {
+    clear_graphs(m);
     if (m->scratch) {
       PF_HIP(hipStreamSynchronize(b->stream));
       PF_HIP(hipFree(m->scratch));
@@ -398,6 +426,9 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   const bool fused_topk = f16 && E == 128 && K == 4;
   const int router_tile = small_dense(D, 8 * SMALL_M) ? 16 : 64;
   const bool route_counts = fused_topk && M > 1024;
+  // up to 16 rows the router is one workgroup, which then also builds the
+  // routing plan (no separate plan kernel: one launch fewer per layer)
+  const bool plan_in_router = fused_topk && router_tile == 16 && M <= 16;
 
   embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
                M, (int)c.vocab, D);
@@ -473,6 +504,10 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
         if (fused_topk) {
           a.topk_idx = s.ridx; a.topk_w = s.rw; a.topk_k = K; a.topk_wscale = 1.0f;
           if (route_counts) a.topk_counts = plan.tile_counts;  // per router tile: the routing plan's counts
+          if (plan_in_router) {
+            a.plan_expert_off = plan.expert_off; a.plan_slot_token = plan.slot_token; a.plan_slot_of = plan.slot_of;
+            a.plan_tiles = plan.tiles; a.plan_num_tiles = plan.num_tiles; a.plan_tile_t = plan.tile_t;
+          }
           if (!m->taps) a.out = nullptr;  // the logits stay in LDS (written only for the debug taps)
         }
         gemm_w4(b, a, XKind::F16, fused_topk ? Epi::F32_TOPK : Epi::F32, false, router_tile, 2, "gemm_router");
@@ -489,7 +524,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     if (route_counts) {
       record_tap(m, "rcount." + tag, plan.tile_counts, (size_t)((M + router_tile - 1) / router_tile) * E * 4);
       moe_route_counts(b, s.ridx, plan.tile_counts, router_tile, M, K, E, plan);
-    } else {
+    } else if (!plan_in_router) {
       moe_route(b, s.ridx, M, K, E, plan);
     }
     record_tap(m, "expert_off." + tag, plan.expert_off, (size_t)(E + 1) * 4);
@@ -599,6 +634,7 @@ pfhip_model* pfhip_model_create(pfhip_backend* b, const pfhip_model_config* cfg,
 void pfhip_model_destroy(pfhip_model* m) {
   if (!m) return;
   hipStreamSynchronize(m->b->stream);
+  clear_graphs(m);
   for (auto& kv : m->w) hipFree(kv.second.p);
   for (auto& t : m->owned) hipFree(t.p);
   if (m->scratch) hipFree(m->scratch);
@@ -620,6 +656,7 @@ int pfhip_model_set_weight(pfhip_model* m, const char* name, const void* bytes, 
     PF_CHECK(n >= it->second && n <= ((it->second + 3) & ~(size_t)3),
              std::string("weight \"") + name + "\" has " + std::to_string(n) + " bytes, expected " +
                  std::to_string(it->second));
+    clear_graphs(m);
     auto& t = m->w[name];
     if (t.p && t.n < n) {
       PF_HIP(hipStreamSynchronize(m->b->stream));
@@ -645,6 +682,7 @@ int pfhip_model_finalize(pfhip_model* m, char* err, size_t cap) {
     const pfhip_model_config& c = m->cfg;
     const size_t D = c.hidden, hd = c.head_dim;
     const size_t Nq = c.heads * hd, Nk = c.kv_heads * hd;
+    clear_graphs(m);
     for (auto& t : m->owned) hipFree(t.p);
     m->owned.clear();
     m->layers.clear();
@@ -712,6 +750,14 @@ int pfhip_model_enable_taps(pfhip_model* m, int on) {
   return 0;
 }
 
+int pfhip_model_enable_graphs(pfhip_model* m, int on) {
+  if (!m) return -1;
+  hipStreamSynchronize(m->b->stream);
+  m->graphs = on != 0;
+  if (!m->graphs) clear_graphs(m);
+  return 0;
+}
+
 int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* mask, uint32_t batch,
                                uint32_t seq_len, pfhip_buffer* logits, char* err, size_t cap) {
   try {
@@ -725,8 +771,44 @@ int pfhip_model_forward_device(pfhip_model* m, pfhip_buffer* ids, pfhip_buffer* 
     PF_CHECK(!mask || mask->size >= M, "mask buffer too small");
     PF_CHECK(logits->size >= M * m->cfg.classes * 4, "logits buffer too small");
     PF_HIP(hipSetDevice(m->b->device));
-    run_forward(m, static_cast<const int32_t*>(ids->ptr), mask ? static_cast<const uint8_t*>(mask->ptr) : nullptr,
-                (int)batch, (int)seq_len, static_cast<float*>(logits->ptr));
+    const int32_t* idp = static_cast<const int32_t*>(ids->ptr);
+    const uint8_t* mkp = mask ? static_cast<const uint8_t*>(mask->ptr) : nullptr;
+    float* lgp = static_cast<float*>(logits->ptr);
+    if (!m->graphs || m->taps || m->b->profiling) {
+      // taps copy to the host mid-forward and profiling brackets launches
+      // with events: both run eagerly
+      run_forward(m, idp, mkp, (int)batch, (int)seq_len, lgp);
+    } else {
+      FwdGraph* g = nullptr;
+      for (auto& e : m->graph_cache)
+        if (e.B == (int)batch && e.T == (int)seq_len && e.ids == idp && e.mask == mkp && e.logits == lgp) g = &e;
+      if (!g) {  // first call of this shape: eagerly (it may grow the scratch and tables, which clears the cache)
+        run_forward(m, idp, mkp, (int)batch, (int)seq_len, lgp);
+        if (m->graph_cache.size() >= 16) {
+          if (m->graph_cache.front().exec) hipGraphExecDestroy(m->graph_cache.front().exec);
+          m->graph_cache.erase(m->graph_cache.begin());
+        }
+        FwdGraph e;
+        e.B = (int)batch; e.T = (int)seq_len; e.ids = idp; e.mask = mkp; e.logits = lgp;
+        m->graph_cache.push_back(e);
+      } else {
+        if (!g->exec) {  // second call: capture the launches once, then replay them
+          hipGraph_t graph = nullptr;
+          PF_HIP(hipStreamBeginCapture(m->b->stream, hipStreamCaptureModeRelaxed));
+          try {
+            run_forward(m, idp, mkp, (int)batch, (int)seq_len, lgp);
+          } catch (...) {
+            if (hipStreamEndCapture(m->b->stream, &graph) == hipSuccess && graph) hipGraphDestroy(graph);
+            throw;
+          }
+          PF_HIP(hipStreamEndCapture(m->b->stream, &graph));
+          const hipError_t ie = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+          hipGraphDestroy(graph);
+          PF_HIP(ie);
+        }
+        PF_HIP(hipGraphLaunch(g->exec, m->b->stream));
+      }
+    }
     PF_HIP(hipStreamSynchronize(m->b->stream));
     prof_flush(m->b);
     return 0;

@@ -125,14 +125,15 @@ struct StagedOut {
 // with the last chunk's register set fixed at compile time (a run-time choice
 // between the two sets made the 128-row tiles spill).
 // W16: the weights are fp16 [N][K] (p.w16; no quantisation, no dequantisation):
-// BASELINE config 3's fp16 router.
+// BASELINE config 3's fp16 router (the 64- and 128-row tiles, and the all-K
+// 16-row tile, whose 5 chunks of fp16 weights take 160 registers).
 struct W16Reg {
   u4_t v[4];
 };
 template <int WF, int BT, int XS, Epi EPI, bool GROUPED, int NW = 4, int CT = 0, bool NORM = false,
           bool EVENC = false, bool W16 = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
-  static_assert(!W16 || (CT == 0 && !GROUPED), "fp16 weights: dense large tiles only");
+  static_assert(!W16 || !GROUPED, "fp16 weights: dense tiles only");
   constexpr int BN = NW * WF * 16;  // weight rows per workgroup
   constexpr int TJ = BT / 16;       // token fragments per wave
   constexpr int XI = BT / (4 * NW);  // 1 KB (4-row) direct loads per wave per plane per chunk
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     }
   };
 
-  [[maybe_unused]] u4_t wall[CT > 0 ? CT : 1][WF];
+  [[maybe_unused]] WR wall[CT > 0 ? CT : 1][WF];
   [[maybe_unused]] uint32_t szall[CT > 0 ? CT : 1][WF];
   if constexpr (CT > 0) {
 #pragma unroll
@@ -647,6 +648,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         }
       }
       }
+      // (the single-tile routing plan: each expert's bitmap of the tile's
+      // rows, after the counters in LDS)
+      [[maybe_unused]] uint32_t* pbits = reinterpret_cast<uint32_t*>(topk_hist + 128);
+      if constexpr (BT == 16) {
+        if (p.plan_slot_of) {  // (uniform)
+          if (tid < 128) pbits[tid] = 0u;
+          __syncthreads();
+        }
+      }
       if (part == 0 && row < rows) {
         if (nan) topk_insertion<4>(at, 128, V, I);
         const size_t t = (size_t)(row0 + row);
@@ -655,10 +665,80 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) atomicAdd(&topk_hist[I[k]], 1);  // order-free: the counts are exact
         }
+        if constexpr (BT == 16) {
+          if (p.plan_slot_of) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) atomicOr(&pbits[I[k]], 1u << row);  // order-free
+          }
+        }
       }
       if (p.topk_counts) {
         __syncthreads();
         if (tid < 128) p.topk_counts[(size_t)(row0 / BT) * 128 + tid] = topk_hist[tid];
+      }
+      if constexpr (BT == 16) {
+        if (p.plan_slot_of) {
+          // The routing plan of the tile's rows (M <= 16, one workgroup),
+          // the outputs of moe_route's single-block kernel: expert e's rows
+          // are its tokens in ascending order (bitmap ranks), experts in
+          // ascending order, tiles of plan_tile_t rows.
+          __syncthreads();
+          int* poff = topk_hist + 256;  // [128] row offsets, [128] tile offsets, [4] wave sums
+          int* ptoff = poff + 128;
+          int* pws = ptoff + 128;
+          int c = 0, ci = 0, ni = 0, n = 0;
+          if (tid < 128) {
+            c = __popc(pbits[tid]);
+            n = (c + p.plan_tile_t - 1) / p.plan_tile_t;
+            ci = c;
+            ni = n;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+              const int a = __shfl_up(ci, o, 64), bb = __shfl_up(ni, o, 64);
+              if (lane >= o) {
+                ci += a;
+                ni += bb;
+              }
+            }
+            if (lane == 63) {
+              pws[2 * wave] = ci;
+              pws[2 * wave + 1] = ni;
+            }
+          }
+          __syncthreads();
+          const int total = pws[0] + pws[2], ntl = pws[1] + pws[3];
+          if (tid < 128) {
+            const int base = (wave == 1 ? pws[0] : 0) + ci - c;
+            poff[tid] = base;
+            ptoff[tid] = (wave == 1 ? pws[1] : 0) + ni - n;
+            p.plan_expert_off[tid] = base;
+          }
+          if (tid == 0) {
+            p.plan_expert_off[128] = total;
+            *p.plan_num_tiles = ntl;
+          }
+          __syncthreads();
+          for (int ti = tid; ti < ntl; ti += 64 * NW) {
+            int lo = 0, hi = 127;
+            while (lo < hi) {
+              const int mid = (lo + hi + 1) >> 1;
+              if (ptoff[mid] <= ti) lo = mid;
+              else hi = mid - 1;
+            }
+            const int tot = (lo < 127 ? poff[lo + 1] : total) - poff[lo];
+            const int r0 = (ti - ptoff[lo]) * p.plan_tile_t;
+            reinterpret_cast<int4*>(p.plan_tiles)[ti] = int4{lo, poff[lo] + r0, min(p.plan_tile_t, tot - r0), 0};
+          }
+          if (part == 0 && row < rows) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int e = I[k];
+              const int pos = poff[e] + __popc(pbits[e] & ((1u << row) - 1u));
+              p.plan_slot_token[pos] = row0 + row;
+              p.plan_slot_of[(size_t)(row0 + row) * 4 + k] = pos;
+            }
+          }
+        }
       }
     }
     return;
@@ -711,10 +791,11 @@ void launch(pfhip_backend* b, const GemmArgs& a, const char* name) {
   // activation buffers: two (double buffering) or all CT chunks, plus the
   // RoPE table's plane when every chunk buffer is taken
   constexpr int NBUF = CT > 0 ? (NORM ? 2 * CT : CT) + (EPI == Epi::ROPE_F16 ? 1 : 0) : 2;
-  // (the top-k epilogue keeps 128 counters after the staged tile)
+  // (the top-k epilogue keeps 128 counters after the staged tile, and on the
+  // 16-row tile the routing plan's 128 bitmaps, 256 offsets and 4 sums)
   const size_t lds = std::max((size_t)NBUF * XS * BT * KC * sizeof(uint16_t),
                               StagedOut<WF, BT, EPI, NW>::OK
-                                  ? StagedOut<WF, BT, EPI, NW>::LDS + (EPI == Epi::F32_TOPK ? 128 * 4 : 0)
+                                  ? StagedOut<WF, BT, EPI, NW>::LDS + (EPI == Epi::F32_TOPK ? 516 * 4 : 0)
                                   : (size_t)0);
   auto go = [&](auto kern) {
     allow_lds(reinterpret_cast<const void*>(kern), lds);
@@ -746,7 +827,7 @@ void dispatch_epi(pfhip_backend* b, const GemmArgs& a, Epi epi, const char* name
       break;
     case Epi::F32_TOPK:
       if constexpr (WF == 2 && (BT == 128 || BT == 64 || (BT == 16 && CT > 0)) && !GROUPED && NW == 4) {
-        if constexpr (CT == 0 && (BT == 64 || BT == 128))
+        if constexpr ((CT == 0 && (BT == 64 || BT == 128)) || (CT == 5 && BT == 16))
           if (a.w16) return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT, false, true>(b, a, name);
         return launch<WF, BT, XS, Epi::F32_TOPK, GROUPED, NW, CT>(b, a, name);
       }
@@ -821,9 +902,11 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
   PF_CHECK(a.N > 0, "gemm_w4: N must be positive");
   PF_CHECK(a.x && ((a.w && a.wsz) || a.w16) && (a.out || epi == Epi::F32_TOPK), "gemm_w4: null operand");
   if (a.w16)
-    PF_CHECK(epi == Epi::F32_TOPK && !grouped && (tile_t == 64 || tile_t == 128) && wf == 2 &&
-                 (reinterpret_cast<uintptr_t>(a.w16) & 15) == 0 && (long)a.N * a.K * 2 < (1L << 31),
-             "gemm_w4: fp16 weights are built for the router top-k tile (64 or 128 rows), 16-byte aligned");
+    PF_CHECK(epi == Epi::F32_TOPK && !grouped && (tile_t == 64 || tile_t == 128 || (tile_t == 16 && a.K == 5 * KC)) &&
+                 wf == 2 && !a.nrm_res && (reinterpret_cast<uintptr_t>(a.w16) & 15) == 0 &&
+                 (long)a.N * a.K * 2 < (1L << 31),
+             "gemm_w4: fp16 weights are built for the router top-k tile (16 rows with K = 640, 64 or 128 rows), "
+             "16-byte aligned");
   PF_CHECK(a.ldx % 8 == 0, "gemm_w4: activation row stride must allow 16-byte loads");
   PF_CHECK((reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0,
            "gemm_w4: activations and weights must be 16-byte aligned");  // (w is null with fp16 weights)
@@ -862,6 +945,10 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
                  a.topk_w && g.out_staged,
              "gemm_w4: the top-k epilogue needs N == 128, K == 4, a 128- or 16-token tile of 128 columns and "
              "16-byte aligned f32 rows");
+  if (a.plan_slot_of)
+    PF_CHECK(epi == Epi::F32_TOPK && tile_t == 16 && a.M >= 1 && a.M <= 16 && a.plan_expert_off && a.plan_slot_token &&
+                 a.plan_tiles && a.plan_num_tiles && a.plan_tile_t >= 1,
+             "gemm_w4: the routing plan is built by the single 16-row router tile (M <= 16), with every plan output");
   if (tile_t == 128 && wf == 4) return dispatch_grouped<4, 128>(b, g, epi, grouped, prof_name);
   // 64-row expert tiles with K = 640 load all five chunks at once (80 KB of
   // LDS, two workgroups per CU): a tile waits for memory once instead of

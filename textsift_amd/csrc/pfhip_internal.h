@@ -131,6 +131,16 @@ struct GemmArgs {
   float topk_wscale = 1.0f;
   // F32_TOPK: when set, [M / BT][128] counts of each tile's rows routed to each expert
   int32_t* topk_counts = nullptr;
+  // F32_TOPK on a single 16-row tile (M <= 16): when plan_slot_of is set, the
+  // same workgroup then builds the routing plan of its rows (the outputs of
+  // moe_route: expert_off [E + 1], slot_token, slot_of, the expert tile list
+  // of plan_tile_t-row tiles and num_tiles), one launch fewer per layer
+  int32_t* plan_expert_off = nullptr;
+  int32_t* plan_slot_token = nullptr;
+  int32_t* plan_slot_of = nullptr;
+  int32_t* plan_tiles = nullptr;
+  int32_t* plan_num_tiles = nullptr;
+  int plan_tile_t = 0;
   // Residual add + RMSNorm on the way in (gemm_w4, 16-token tile, K == 640):
   // x is the fp16 O projection output o; the kernel forms h2 = fp16(o + res)
   // and xn = fp16(h2 * inv_rms(o + res) * gamma), writes both, and multiplies xn.

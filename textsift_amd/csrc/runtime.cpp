@@ -180,7 +180,7 @@ static void run_matmul(pfhip_backend* b, pfhip_buffer* const* bs, const uint8_t*
 // router_t: the router weight transposed once beforehand ([E][D], the
 // transpose_f16 dispatch), for 128 experts and top-4: the chain the forward
 // runs -- one router GEMM whose epilogue selects the experts and counts each
-// 64-row tile's picks per expert, then one kernel for the plan (above 1024
+// router tile's picks per expert, then one kernel for the plan (above 1024
 // tokens; below, the single-workgroup plan kernel): five launches in all.
 // Otherwise (router W [D][E]): transpose, router GEMM, top-k, plan, then the
 // same expert kernels.
@@ -201,7 +201,11 @@ static void moe_ffn_fp16(pfhip_backend* b, const uint16_t* x, const uint16_t* rw
   MoePlan m = moe_plan_carve(s, T, K, E, et.t);
   if (router_t) {
     PF_CHECK(E == 128 && K == 4 && D % 128 == 0, "moe_ffn_w4: the transposed router is built for 128 experts, top-4");
-    constexpr int RT = 64;  // router rows per tile (divides the plan's 1024-token blocks)
+    // router rows per tile (divides the plan's 1024-token blocks): the all-K
+    // 16-row tile up to 16384 rows, as the forward chooses it (config 3's
+    // 2048 rows: 128 workgroups that wait for memory once, instead of 32
+    // that wait once per K chunk)
+    const int RT = T <= 16384 && D == 5 * 128 ? 16 : 64;
     GemmArgs r;
     r.x = x; r.ldx = D; r.w16 = rw; r.bias = rb;
     r.out = nullptr; r.ldo = E; r.M = T; r.N = E; r.K = D;
