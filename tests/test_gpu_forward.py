@@ -217,6 +217,24 @@ def test_full_model_small_t_vs_oracle(full_ref):
         be.dispose()
 
 
+def test_small_t_fused_steps_are_exact(full_ref):
+    """Up to 16 rows the router's workgroup builds the routing plan; above,
+    the plan kernel does. A sequence's logits are the same bits either way:
+    each sequence of a 3 x 8 batch (24 rows, the plan kernel) equals its own
+    1 x 8 forward (8 rows, the plan in the router)."""
+    w = full_ref[0]
+    be = HipBackend(w)
+    be.warmup()
+    try:
+        ids = synth.tagged_token_ids(77, 24).reshape(3, 8)
+        batch = be.forward_batch(ids)
+        for b in range(3):
+            one = be.forward(ids[b], np.ones(8, np.uint8)).as_matrix()
+            assert np.array_equal(one.view(np.uint32), batch[b].view(np.uint32)), f"sequence {b}"
+    finally:
+        be.dispose()
+
+
 @pytest.mark.parametrize("precision", PRECISIONS, ids=["fp16", "split"])
 def test_full_batch_16x2048(full_ref, precision):
     """The benchmarked launch set (BASELINE config 5 at its stated batch):

@@ -294,6 +294,27 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       sc[f] = h2_t{pr.y, pr.y};
     }
     const _Float16* xb = xs_lds + buf * XS * PLANE;
+    if constexpr (TJ == 1 && XS == 1) {
+      // one token fragment (the 16-row tiles): the chunk's four activation
+      // fragments are read before its MFMAs, so the LDS latency is paid once
+      // per chunk instead of once per step (the steps are otherwise a serial
+      // chain of LDS read, wait, MFMA)
+      h8_t xh[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xh[j] = *reinterpret_cast<const h8_t*>(xb + l16 * KC + (((4 * lg + j) ^ l16) << 3));
+      __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink the reads next to their MFMAs)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int f = 0; f < WF; ++f) {
+          h8_t wd;
+          if constexpr (W16) wd = __builtin_bit_cast(h8_t, wr[f].v[j]);
+          else wd = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
+          acc[f][0] = mfma16x16x32(wd, xh[j], acc[f][0]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
@@ -326,6 +347,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       load_x(c, c);
       load_w(c, wall[c], szall[c]);
     }
+    [[maybe_unused]] u4_t gam[CT];
     if constexpr (NORM) {
       // the residual rows into buffers CT .. 2 CT - 1, in the same layout
 #pragma unroll
@@ -333,6 +355,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
         for (int m = 0; m < XI; ++m)
           copy16_to_lds(p.nrm_res + xoff[m] + c * KC, (lds_ptr_t)(xs_lds + (CT + c) * PLANE + (m * NW + wave) * 512));
+      // and this thread's gamma units (see below), under the same wait
+      const int q = tid & 15;
+#pragma unroll
+      for (int f = 0; f < CT; ++f)
+        gam[f] = *reinterpret_cast<const u4_t*>(p.nrm_gamma + (5 * (q >> 1) + f) * 16 + 8 * (q & 1));
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -381,9 +408,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       __syncthreads();  // every thread has read its o and residual units
 #pragma unroll
       for (int f = 0; f < CT; ++f) {
-        const u4_t gw = *reinterpret_cast<const u4_t*>(p.nrm_gamma + colf[f]);
         const h8_t h8 = __builtin_bit_cast(h8_t, hs[f]);
-        const h8_t g8 = __builtin_bit_cast(h8_t, gw);
+        const h8_t g8 = __builtin_bit_cast(h8_t, gam[f]);
         float y[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) y[i] = (float)h8[i] * inv_rms * (float)g8[i];

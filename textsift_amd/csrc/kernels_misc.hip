@@ -7,6 +7,7 @@
 #include "epilogue.h"
 #include "pfhip_internal.h"
 #include "topk.h"
+#include "combine.h"
 
 namespace pf {
 
@@ -83,26 +84,6 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ q, co
 // Widening is the reference's bit trick (wasm_h2f).
 constexpr int MAXJ = 4;  // 256-element slices per row
 
-// Output forms of a normalised row: fp16, f32, or the f32 value as hi/lo fp16 planes.
-enum OutMode { OUT_F16 = 0, OUT_F32 = 1, OUT_SPLIT = 2 };
-
-
-__device__ __forceinline__ void h4_to_f(u2_t w, float v[4]) { h4_widen(w, v); }
-
-template <int MODE>
-__device__ __forceinline__ void put4(void* out, uint16_t* out_lo, size_t i, const float y[4]) {
-  if constexpr (MODE == OUT_F32) {
-    *reinterpret_cast<f4_t*>(static_cast<float*>(out) + i) = f4_t{y[0], y[1], y[2], y[3]};
-  } else if constexpr (MODE == OUT_F16) {
-    *reinterpret_cast<u2_t*>(static_cast<uint16_t*>(out) + i) = to_f16x4(y);
-  } else {
-    uint16_t h[4], l[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) split_hilo(y[r], h[r], l[r]);
-    *reinterpret_cast<u2_t*>(static_cast<uint16_t*>(out) + i) = pack4(h);
-    *reinterpret_cast<u2_t*>(out_lo + i) = pack4(l);
-  }
-}
 
 template <int MODE>
 __global__ __launch_bounds__(256) void k_rms_norm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ g,
@@ -836,103 +817,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(const int32_t* __restrict__
                                                      const uint16_t* __restrict__ gamma,
                                                      uint16_t* __restrict__ norm_hi, uint16_t* __restrict__ norm_lo,
                                                      int T, int D, float eps) {
-  const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (t >= T) return;
-  int ek[K], sk[K];
-  float wk[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    ek[k] = idx[(size_t)t * K + k];
-    wk[k] = w[(size_t)t * K + k];
-    sk[k] = slot_of[(size_t)t * K + k];
-  }
-  // ascending expert id (ids are distinct): a fixed compare-exchange network
-#pragma unroll
-  for (int a = 1; a < K; ++a)
-#pragma unroll
-    for (int j = a; j > 0; --j) {
-      const bool sw = ek[j] < ek[j - 1];
-      const int e0 = ek[j - 1], e1 = ek[j], s0 = sk[j - 1], s1 = sk[j];
-      const float w0 = wk[j - 1], w1 = wk[j];
-      ek[j - 1] = sw ? e1 : e0;
-      ek[j] = sw ? e0 : e1;
-      sk[j - 1] = sw ? s1 : s0;
-      sk[j] = sw ? s0 : s1;
-      wk[j - 1] = sw ? w1 : w0;
-      wk[j] = sw ? w0 : w1;
-    }
-  const size_t base = (size_t)t * D;
-  // every load of the row is issued before any is used
-  f4_t yv[NJ][K];
-  u2_t rw[NJ], gw[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int d = 4 * lane + 256 * j;
-    if (d < D) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        if constexpr (Y16) {
-          // read once: non-temporal, so the 168 MB of expert outputs do not
-          // push the next GEMM's activations and weights out of the caches
-          // (the QKV GEMM that follows: 68.5 -> 66 us; forward -1 %)
-          const h4_t h = __builtin_bit_cast(
-              h4_t, __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(static_cast<const uint16_t*>(y) +
-                                                                             (size_t)sk[k] * D + d)));
-          yv[j][k] = f4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
-        } else {
-          yv[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)sk[k] * D + d);
-        }
-      }
-      if constexpr (RES) rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
-      else rw[j] = u2_t{0u, 0u};
-      if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
-    }
-  }
-  u2_t hs[NJ];
-  float ss = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int d = 4 * lane + 256 * j;
-    hs[j] = u2_t{0u, 0u};
-    if (d < D) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], yv[j][k][r], acc[r]);
-      const u2_t m = to_f16x4(acc);
-      if (moe_out) *reinterpret_cast<u2_t*>(moe_out + base + d) = m;
-      float mv[4], rv[4], sv[4];
-      h4_to_f(m, mv);
-      h4_to_f(rw[j], rv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sv[r] = rv[r] + mv[r];
-      hs[j] = to_f16x4(sv);
-      *reinterpret_cast<u2_t*>(h_out + base + d) = hs[j];
-      float hv[4];
-      h4_to_f(hs[j], hv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ss += hv[r] * hv[r];
-    }
-  }
-  if constexpr (NMODE >= 0) {
-    // the next block's rms_norm_fp16_to_f32 on the new residual row (:220-270)
-    ss = wave_sum(ss);
-    const float inv_rms = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int d = 4 * lane + 256 * j;
-      if (d < D) {
-        float hv[4], gm[4], yo[4];
-        h4_to_f(hs[j], hv);
-        h4_to_f(gw[j], gm);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yo[r] = hv[r] * inv_rms * gm[r];
-        put4<NMODE>(norm_hi, norm_lo, base + d, yo);
-      }
-    }
-  }
+  moe_combine_row<NMODE, K, NJ, Y16, RES>(t, threadIdx.x & 63, idx, w, slot_of, y, residual, moe_out, h_out, gamma,
+                                          norm_hi, norm_lo, D, eps);
 }
 
 template <int NMODE, bool Y16, bool RES>
