@@ -3,6 +3,8 @@
 // kernels_misc.hip, callable from any kernel that holds a wave per token).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "epilogue.h"
 
@@ -31,44 +33,65 @@ __device__ __forceinline__ void put4(void* out, uint16_t* out_lo, size_t i, cons
 }
 
 
-// One token's combine (k_moe_combine below): the wave of lane `lane` sums
-// token t's K expert outputs (in slot order of slot_of) with its routing
-// weights in ascending expert id, adds the residual and, for NMODE >= 0,
-// writes the next block's RMSNorm of the new residual row.
-template <int NMODE, int K, int NJ, bool Y16, bool RES>
-__device__ __forceinline__ void moe_combine_row(int t, int lane, const int32_t* __restrict__ idx,
-                                                const float* __restrict__ w, const int32_t* __restrict__ slot_of,
-                                                const void* __restrict__ y, const uint16_t* __restrict__ residual,
-                                                uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
-                                                const uint16_t* __restrict__ gamma, uint16_t* __restrict__ norm_hi,
-                                                uint16_t* __restrict__ norm_lo, int D, float eps) {
-  int ek[K], sk[K];
-  float wk[K];
+// One token's combine (k_moe_combine in kernels_misc.hip), in three steps so
+// that a wave can keep several tokens' loads in flight: comb_index (the
+// token's K expert ids, routing weights and slots, sorted by ascending expert
+// id), comb_load (every load of the row, issued before any is used) and
+// comb_finish (sum the K expert outputs with fused multiply-adds in ascending
+// expert id, add the residual, and for NMODE >= 0 the next block's RMSNorm
+// of the new residual row). Lane `lane` of the token's wave holds elements
+// 4 lane + 256 j .. +3. The results go to store_m(d, moe out), store_h(d,
+// new residual) and store_n(d, norm values), so every caller gets the same
+// bits.
+template <int K>
+struct CombIdx {
+  int e[K], s[K];
+  float w[K];
+};
+
+template <int K>
+__device__ __forceinline__ CombIdx<K> comb_index(int t, const int32_t* __restrict__ idx, const float* __restrict__ w,
+                                                 const int32_t* __restrict__ slot_of) {
+  CombIdx<K> c;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    ek[k] = idx[(size_t)t * K + k];
-    wk[k] = w[(size_t)t * K + k];
-    sk[k] = slot_of[(size_t)t * K + k];
+    c.e[k] = idx[(size_t)t * K + k];
+    c.w[k] = w[(size_t)t * K + k];
+    c.s[k] = slot_of[(size_t)t * K + k];
   }
   // ascending expert id (ids are distinct): a fixed compare-exchange network
 #pragma unroll
   for (int a = 1; a < K; ++a)
 #pragma unroll
     for (int j = a; j > 0; --j) {
-      const bool sw = ek[j] < ek[j - 1];
-      const int e0 = ek[j - 1], e1 = ek[j], s0 = sk[j - 1], s1 = sk[j];
-      const float w0 = wk[j - 1], w1 = wk[j];
-      ek[j - 1] = sw ? e1 : e0;
-      ek[j] = sw ? e0 : e1;
-      sk[j - 1] = sw ? s1 : s0;
-      sk[j] = sw ? s0 : s1;
-      wk[j - 1] = sw ? w1 : w0;
-      wk[j] = sw ? w0 : w1;
+      const bool sw = c.e[j] < c.e[j - 1];
+      const int e0 = c.e[j - 1], e1 = c.e[j], s0 = c.s[j - 1], s1 = c.s[j];
+      const float w0 = c.w[j - 1], w1 = c.w[j];
+      c.e[j - 1] = sw ? e1 : e0;
+      c.e[j] = sw ? e0 : e1;
+      c.s[j - 1] = sw ? s1 : s0;
+      c.s[j] = sw ? s0 : s1;
+      c.w[j - 1] = sw ? w1 : w0;
+      c.w[j] = sw ? w0 : w1;
     }
+  return c;
+}
+
+// the loaded operands of one token's row: expert outputs (fp16 bits with
+// Y16, else f32), residual and gamma units
+template <int K, int NJ, bool Y16>
+struct CombRow {
+  std::conditional_t<Y16, u2_t, f4_t> y[NJ][K];
+  u2_t r[NJ], g[NJ];
+};
+
+template <int NMODE, int K, int NJ, bool Y16, bool RES>
+__device__ __forceinline__ CombRow<K, NJ, Y16> comb_load(int t, int lane, const CombIdx<K>& c,
+                                                         const void* __restrict__ y,
+                                                         const uint16_t* __restrict__ residual,
+                                                         const uint16_t* __restrict__ gamma, int D) {
+  CombRow<K, NJ, Y16> L;
   const size_t base = (size_t)t * D;
-  // every load of the row is issued before any is used
-  f4_t yv[NJ][K];
-  u2_t rw[NJ], gw[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int d = 4 * lane + 256 * j;
@@ -79,19 +102,23 @@ __device__ __forceinline__ void moe_combine_row(int t, int lane, const int32_t* 
           // read once: non-temporal, so the 168 MB of expert outputs do not
           // push the next GEMM's activations and weights out of the caches
           // (the QKV GEMM that follows: 68.5 -> 66 us; forward -1 %)
-          const h4_t h = __builtin_bit_cast(
-              h4_t, __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(static_cast<const uint16_t*>(y) +
-                                                                             (size_t)sk[k] * D + d)));
-          yv[j][k] = f4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+          L.y[j][k] = __builtin_nontemporal_load(
+              reinterpret_cast<const u2_t*>(static_cast<const uint16_t*>(y) + (size_t)c.s[k] * D + d));
         } else {
-          yv[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)sk[k] * D + d);
+          L.y[j][k] = *reinterpret_cast<const f4_t*>(static_cast<const float*>(y) + (size_t)c.s[k] * D + d);
         }
       }
-      if constexpr (RES) rw[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
-      else rw[j] = u2_t{0u, 0u};
-      if constexpr (NMODE >= 0) gw[j] = *reinterpret_cast<const u2_t*>(gamma + d);
+      if constexpr (RES) L.r[j] = *reinterpret_cast<const u2_t*>(residual + base + d);
+      else L.r[j] = u2_t{0u, 0u};
+      if constexpr (NMODE >= 0) L.g[j] = *reinterpret_cast<const u2_t*>(gamma + d);
     }
   }
+  return L;
+}
+
+template <int NMODE, int K, int NJ, bool Y16, class SM, class SH, class SN>
+__device__ __forceinline__ void comb_finish(int lane, const CombIdx<K>& c, const CombRow<K, NJ, Y16>& L, int D,
+                                            float eps, SM store_m, SH store_h, SN store_n) {
   u2_t hs[NJ];
   float ss = 0.0f;
 #pragma unroll
@@ -99,20 +126,30 @@ __device__ __forceinline__ void moe_combine_row(int t, int lane, const int32_t* 
     const int d = 4 * lane + 256 * j;
     hs[j] = u2_t{0u, 0u};
     if (d < D) {
+      f4_t yv[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if constexpr (Y16) {
+          const h4_t h = __builtin_bit_cast(h4_t, L.y[j][k]);
+          yv[k] = f4_t{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+        } else {
+          yv[k] = L.y[j][k];
+        }
+      }
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int k = 0; k < K; ++k)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(wk[k], yv[j][k][r], acc[r]);
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(c.w[k], yv[k][r], acc[r]);
       const u2_t m = to_f16x4(acc);
-      if (moe_out) *reinterpret_cast<u2_t*>(moe_out + base + d) = m;
+      store_m(d, m);
       float mv[4], rv[4], sv[4];
       h4_to_f(m, mv);
-      h4_to_f(rw[j], rv);
+      h4_to_f(L.r[j], rv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) sv[r] = rv[r] + mv[r];
       hs[j] = to_f16x4(sv);
-      *reinterpret_cast<u2_t*>(h_out + base + d) = hs[j];
+      store_h(d, hs[j]);
       float hv[4];
       h4_to_f(hs[j], hv);
 #pragma unroll
@@ -129,13 +166,33 @@ __device__ __forceinline__ void moe_combine_row(int t, int lane, const int32_t* 
       if (d < D) {
         float hv[4], gm[4], yo[4];
         h4_to_f(hs[j], hv);
-        h4_to_f(gw[j], gm);
+        h4_to_f(L.g[j], gm);
 #pragma unroll
         for (int r = 0; r < 4; ++r) yo[r] = hv[r] * inv_rms * gm[r];
-        put4<NMODE>(norm_hi, norm_lo, base + d, yo);
+        store_n(d, yo);
       }
     }
   }
+}
+
+// One token's combine with its results in global memory (the combine kernel).
+template <int NMODE, int K, int NJ, bool Y16, bool RES>
+__device__ __forceinline__ void moe_combine_row(int t, int lane, const int32_t* __restrict__ idx,
+                                                const float* __restrict__ w, const int32_t* __restrict__ slot_of,
+                                                const void* __restrict__ y, const uint16_t* __restrict__ residual,
+                                                uint16_t* __restrict__ moe_out, uint16_t* __restrict__ h_out,
+                                                const uint16_t* __restrict__ gamma, uint16_t* __restrict__ norm_hi,
+                                                uint16_t* __restrict__ norm_lo, int D, float eps) {
+  const CombIdx<K> c = comb_index<K>(t, idx, w, slot_of);
+  const CombRow<K, NJ, Y16> L = comb_load<NMODE, K, NJ, Y16, RES>(t, lane, c, y, residual, gamma, D);
+  const size_t base = (size_t)t * D;
+  comb_finish<NMODE, K, NJ, Y16>(
+      lane, c, L, D, eps,
+      [&](int d, u2_t m) {
+        if (moe_out) *reinterpret_cast<u2_t*>(moe_out + base + d) = m;
+      },
+      [&](int d, u2_t hv) { *reinterpret_cast<u2_t*>(h_out + base + d) = hv; },
+      [&](int d, const float* yo) { put4<NMODE>(norm_hi, norm_lo, base + d, yo); });
 }
 
 }  // namespace
