@@ -139,6 +139,13 @@ __device__ __forceinline__ u2_t rope_f16x4_native(const float v[4], h4_t t) {
 
 // Stores 4 packed fp16 values at out[orow][n..n+3] (columns past N dropped).
 __device__ __forceinline__ void store_f16x4(const GemmArgs& p, size_t orow, int n, u2_t hv) {
+  if (p.out_f32w) {
+    float* of = p.out_f32w + orow * p.ldo + n;
+    const uint32_t w2[2] = {hv.x, hv.y};
+    for (int r = 0; r < 4; ++r)
+      if (n + r < p.N) of[r] = hw_h2f((uint16_t)(w2[r >> 1] >> (16 * (r & 1))));
+    if (!p.out) return;
+  }
   uint16_t* o = static_cast<uint16_t*>(p.out) + orow * p.ldo + n;
   if (n + 3 < p.N) {
     *reinterpret_cast<u2_t*>(o) = hv;

@@ -576,6 +576,10 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
     a.out = s.logits16; a.ldo = C; a.M = M; a.N = C; a.K = D;
     if (f16) {
       a.w = reinterpret_cast<const uint8_t*>(m->score4.w); a.wsz = m->score4.sz;
+      // wasm.ts:776-796 widens the fp16 logits IEEE-correctly: the epilogue
+      // stores them widened (the fp16 copy only for the taps)
+      a.out_f32w = logits_out ? logits_out : s.logits;
+      if (!m->taps) a.out = nullptr;
       gemm_w4(b, a, XKind::F16, Epi::F16, false, small_dense(D, 2 * SMALL_M) ? 16 : 64, 1, "gemm_classifier");
     } else {
       gemm_int4(b, a, XKind::SPLIT, Epi::F16, false, 128, "gemm_classifier");
@@ -583,7 +587,7 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   }
   record_tap(m, "logits16", s.logits16, (size_t)M * C * 2);
   // wasm.ts:776-796 widens the fp16 logits IEEE-correctly
-  cast_f16_f32_ieee(b, s.logits16, logits_out ? logits_out : s.logits, (size_t)M * C);
+  if (!f16) cast_f16_f32_ieee(b, s.logits16, logits_out ? logits_out : s.logits, (size_t)M * C);
 }
 
 extern "C" {

@@ -926,7 +926,8 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
              const char* prof_name) {
   PF_CHECK(a.K > 0 && a.K % KC == 0, "gemm_w4: K must be a positive multiple of 128");
   PF_CHECK(a.N > 0, "gemm_w4: N must be positive");
-  PF_CHECK(a.x && ((a.w && a.wsz) || a.w16) && (a.out || epi == Epi::F32_TOPK), "gemm_w4: null operand");
+  PF_CHECK(a.x && ((a.w && a.wsz) || a.w16) && (a.out || epi == Epi::F32_TOPK || a.out_f32w), "gemm_w4: null operand");
+  if (a.out_f32w) PF_CHECK(epi == Epi::F16 && !grouped, "gemm_w4: the widened f32 output is for the dense F16 epilogue");
   if (a.w16)
     PF_CHECK(epi == Epi::F32_TOPK && !grouped && (tile_t == 64 || tile_t == 128 || (tile_t == 16 && a.K == 5 * KC)) &&
                  wf == 2 && !a.nrm_res && (reinterpret_cast<uintptr_t>(a.w16) & 15) == 0 &&
@@ -962,7 +963,8 @@ void gemm_w4(pfhip_backend* b, const GemmArgs& a, XKind xk, Epi epi, bool groupe
     g.out_staged = (epi == Epi::F32 || epi == Epi::F32_TOPK || epi == Epi::F16 || epi == Epi::ROPE_F16 ||
                     epi == Epi::SWIGLU_F16) &&
                    ocols % (16 / esz) == 0 && (a.ldo * esz) % 16 == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && (epi != Epi::SWIGLU_F16 || a.N % 16 == 0);
+                   (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && (epi != Epi::SWIGLU_F16 || a.N % 16 == 0) &&
+                   !a.out_f32w;
   }
   PF_CHECK(epi != Epi::SWIGLU_SPLIT, "gemm_w4: SwiGLU output is fp16");
   if (epi == Epi::F32_TOPK)

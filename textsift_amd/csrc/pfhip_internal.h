@@ -112,6 +112,10 @@ struct GemmArgs {
   const uint16_t* w16 = nullptr;
   void* out = nullptr;
   uint16_t* out_lo = nullptr;    // SWIGLU_SPLIT: lo plane of the output
+  // F16 epilogue with direct stores: the fp16-rounded outputs also widened
+  // to f32 here ([M][ldo], IEEE widening, exact), out may then be NULL (the
+  // classifier's logits without a separate cast)
+  float* out_f32w = nullptr;
   int ldo = 0;
   int M = 0, N = 0, K = 0;
   // grouped (per-expert) mode
