@@ -617,8 +617,16 @@ void banded_attention(pfhip_backend* b, const AttnArgs& a) {
                ((uintptr_t)a.out & 7) == 0,
            "banded_attention: operands must be 16-byte aligned");
   if (a.B <= 0 || a.T <= 0) return;
-  if (a.head_dim == 64) pick_nch<64>(b, a);
-  else pick_nch<32>(b, a);
+  // A sequence no longer than the window attends to all of itself: any window
+  // of at least T - 1 gives every query the same keys. The GPU-shader kernel
+  // then runs with the smallest such window that differs from the given one
+  // by a multiple of 32: its 32-key chunks hold the same keys in the same
+  // order (so the results are the same bits), and the tile stages and skips
+  // fewer of them (T = 7: 160 instead of 416 staged rows, four waves).
+  AttnArgs e = a;
+  if (a.hw_exp && a.T - 1 < a.window) e.window = a.window - 32 * ((a.window - (a.T - 1)) / 32);
+  if (a.head_dim == 64) pick_nch<64>(b, e);
+  else pick_nch<32>(b, e);
 }
 
 }  // namespace pf
