@@ -278,7 +278,7 @@ BLAS_SHAPES = [  # (kernel of this build, what its launch also does)
     ("gemm_o_add_rmsnorm", "int4 W, bias, residual add, RMSNorm"),
     ("gemm_router", "int4 W, bias, f32 out, top-4 + softmax"),
     ("gemm_moe_gate_up", "int4 W, 128 experts grouped, bias, SwiGLU"),
-    ("gemm_moe_down", "int4 W, 128 experts grouped, bias, f32 out"),
+    ("gemm_moe_down", "int4 W, 128 experts grouped, bias, fp16 out"),
 ]
 
 
