@@ -173,6 +173,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     if (rows <= 0) return;
   }
   const int n0 = nt * BN;
+  // Weight fragments per wave: WF, or WF / 2 when the rows from n0 to N fit
+  // in half the tile (the last tile of an N that is not a multiple of BN:
+  // down's 640 = 2.5 x 256, QKV's 1152 = 4.5 x 256). Fragment f of wave w
+  // holds rows n0 + (w nf + f) 16 .. + 15, so a half tile spreads its rows
+  // over every wave and takes half the time. A wave whose rows all lie past
+  // N loads no weights and issues no dequantisation or MFMAs; it still
+  // copies its share of the activations and joins every barrier. Both are
+  // wave-uniform. (The all-K tiles, CT > 0, keep every wave busy: guarding
+  // their loads spills.)
+  constexpr bool HALF = CT == 0 && WF % 2 == 0 && !W16 && StagedOut<WF, BT, EPI, NW>::NP == 1 &&
+                        EPI == Epi::F16 && GROUPED;
+  const bool half = HALF && p.N - n0 <= NW * (WF / 2) * 16;
+  const int nf = half ? WF / 2 : WF;
+  const bool idle = CT == 0 && n0 + wave * nf * 16 >= p.N;
   const int K = p.K;
   const int C = K / KC;
   const int kd = K >> 3;   // dwords per packed weight row
@@ -192,7 +206,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   uint32_t woff[WF], soff[WF];
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
-    const int n = min(n0 + (wave * WF + f) * 16 + l16, p.N - 1);
+    const int n = min(n0 + (wave * nf + f) * 16 + l16, p.N - 1);
     woff[f] = W16 ? (uint32_t)(n * K + lg * 32) * 2u : (uint32_t)(n * kd + lg * 4) * 4u;
     soff[f] = (uint32_t)(n * nb + lg) * 4u;
   }
@@ -226,9 +240,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   using WR = std::conditional_t<W16, W16Reg, u4_t>;
   WR wraw[WF], wnext[WF];
   uint32_t sz[WF], sznext[WF];
-  auto load_w = [&](int c, WR* wr, uint32_t* s) {
+  // (nfc: std::integral_constant, the fragments loaded: WF, or WF / 2 in a half tile)
+  auto load_w = [&](auto nfc, int c, WR* wr, uint32_t* s) {
 #pragma unroll
-    for (int f = 0; f < WF; ++f) {
+    for (int f = 0; f < decltype(nfc)::value; ++f) {
       if constexpr (W16) {
         // chunk c: this lane's 32 consecutive values (64 bytes), one 16-byte unit per MFMA step
 #pragma unroll
@@ -250,7 +265,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   const uint16_t* __restrict__ BIAS = p.bias ? p.bias + (size_t)expert * p.bias_gs : nullptr;
   int ncol[WF];
 #pragma unroll
-  for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * WF + f) * 16 + 4 * lg;
+  for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * nf + f) * 16 + 4 * lg;
   f4_t acc[WF][TJ];
   {
     u2_t braw[WF];
@@ -284,10 +299,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   }
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
-  auto compute = [&](int buf, const WR (&wr)[WF], const uint32_t (&szc)[WF]) {
+  // (fragments 0 .. nfc - 1)
+  auto compute = [&](auto nfc, int buf, const WR (&wr)[WF], const uint32_t (&szc)[WF]) {
+    constexpr int NF = decltype(nfc)::value;
     h2_t off[WF], offh[WF], sc[WF];
 #pragma unroll
-    for (int f = 0; f < WF; ++f) {
+    for (int f = 0; f < NF; ++f) {
       const h2_t pr = __builtin_bit_cast(h2_t, szc[f]);
       off[f] = h2_t{pr.x, pr.x};
       offh[f] = off_high(off[f]);
@@ -306,7 +323,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
 #pragma unroll
-        for (int f = 0; f < WF; ++f) {
+        for (int f = 0; f < NF; ++f) {
           h8_t wd;
           if constexpr (W16) wd = __builtin_bit_cast(h8_t, wr[f].v[j]);
           else wd = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
@@ -319,7 +336,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     for (int j = 0; j < 4; ++j) {
       h8_t wd[WF];
 #pragma unroll
-      for (int f = 0; f < WF; ++f) {
+      for (int f = 0; f < NF; ++f) {
         if constexpr (W16) wd[f] = __builtin_bit_cast(h8_t, wr[f].v[j]);
         else wd[f] = dequant_fold(wr[f][j], off[f], offh[f], sc[f]);
       }
@@ -329,11 +346,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         const int o = (16 * tj + l16) * KC + unit;
         const h8_t xh = *reinterpret_cast<const h8_t*>(xb + o);
 #pragma unroll
-        for (int f = 0; f < WF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xh, acc[f][tj]);
+        for (int f = 0; f < NF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xh, acc[f][tj]);
         if constexpr (XS == 2) {
           const h8_t xl = *reinterpret_cast<const h8_t*>(xb + PLANE + o);
 #pragma unroll
-          for (int f = 0; f < WF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xl, acc[f][tj]);
+          for (int f = 0; f < NF; ++f) acc[f][tj] = mfma16x16x32(wd[f], xl, acc[f][tj]);
         }
       }
     }
@@ -345,7 +362,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
       load_x(c, c);
-      load_w(c, wall[c], szall[c]);
+      load_w(std::integral_constant<int, WF>{}, c, wall[c], szall[c]);
     }
     [[maybe_unused]] u4_t gam[CT];
     if constexpr (NORM) {
@@ -428,29 +445,34 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     // (wnext, sznext) for odd c, its activations in LDS buffer c & 1: the
     // loop is unrolled by two so that neither the register sets nor the
     // buffer addresses change at run time (no register copies per chunk)
-    auto step = [&](int c, int buf, const WR (&wc)[WF], const uint32_t (&scc)[WF], WR (&wn)[WF],
-                    uint32_t (&sn)[WF]) {
+    // (a half tile runs its own copy of the loop, over WF / 2 fragments)
+    auto kloop = [&](auto nfc) {
+      auto step = [&](int c, int buf, const WR (&wc)[WF], const uint32_t (&scc)[WF], WR (&wn)[WF],
+                      uint32_t (&sn)[WF]) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        load_x(c + 1, buf ^ 1);
+        if (!idle) load_w(nfc, c + 1, wn, sn);
+        // the expert GEMMs raise the wave's issue priority over the chunk's
+        // MFMAs and dequantisation (and drop it for the loads and the barrier):
+        // gate_up 235 -> 229 us, down -1 us; the dense QKV GEMM got slower with it
+        if constexpr (GROUPED) __builtin_amdgcn_s_setprio(1);
+        if (!idle) compute(nfc, buf, wc, scc);
+        if constexpr (GROUPED) __builtin_amdgcn_s_setprio(0);
+      };
+      load_x(0, 0);
+      if (!idle) load_w(nfc, 0, wraw, sz);
+      int c = 0;
+      for (; c + 2 < C; c += 2) {
+        step(c, 0, wraw, sz, wnext, sznext);
+        step(c + 1, 1, wnext, sznext, wraw, sz);
+      }
+      if constexpr (EVENC) step(c, 0, wraw, sz, wnext, sznext);  // the last chunk, C - 1, is then in set B
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      load_x(c + 1, buf ^ 1);
-      load_w(c + 1, wn, sn);
-      // the expert GEMMs raise the wave's issue priority over the chunk's
-      // MFMAs and dequantisation (and drop it for the loads and the barrier):
-      // gate_up 235 -> 229 us, down -1 us; the dense QKV GEMM got slower with it
-      if constexpr (GROUPED) __builtin_amdgcn_s_setprio(1);
-      compute(buf, wc, scc);
-      if constexpr (GROUPED) __builtin_amdgcn_s_setprio(0);
     };
-    load_x(0, 0);
-    load_w(0, wraw, sz);
-    int c = 0;
-    for (; c + 2 < C; c += 2) {
-      step(c, 0, wraw, sz, wnext, sznext);
-      step(c + 1, 1, wnext, sznext, wraw, sz);
-    }
-    if constexpr (EVENC) step(c, 0, wraw, sz, wnext, sznext);  // the last chunk, C - 1, is then in set B
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    if (half) kloop(std::integral_constant<int, HALF ? WF / 2 : WF>{});
+    else kloop(std::integral_constant<int, WF>{});
   }
 
   // ---- RoPE operands, loaded before the last chunk's MFMAs so that their
@@ -478,10 +500,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 
   if constexpr (CT > 0) {
 #pragma unroll
-    for (int c = 0; c < CT; ++c) compute(c, wall[c], szall[c]);
-  } else {
-    if constexpr (EVENC) compute(1, wnext, sznext);
-    else compute(0, wraw, sz);
+    for (int c = 0; c < CT; ++c) compute(std::integral_constant<int, WF>{}, c, wall[c], szall[c]);
+  } else if (!idle) {
+    auto last = [&](auto nfc) {
+      if constexpr (EVENC) compute(nfc, 1, wnext, sznext);
+      else compute(nfc, 0, wraw, sz);
+    };
+    if (half) last(std::integral_constant<int, HALF ? WF / 2 : WF>{});
+    else last(std::integral_constant<int, WF>{});
   }
   // the SwiGLU epilogue's clamp reads the accumulators with inline assembly
   if constexpr (EPI == Epi::SWIGLU_F16) {
@@ -506,7 +532,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     if constexpr (!SO::F32OUT) {
 #pragma unroll
       for (int f = 0; f < WF; ++f) {
-        const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
+        const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * nf + f) * 16 < p.rope_cols;
         const int pidx = (ncol[f] & 63) >> 1;
 #pragma unroll
         for (int tj = 0; tj < TJ; ++tj) {
@@ -540,7 +566,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
         for (int tj = 0; tj < TJ; ++tj) {
           const int row = 16 * tj + l16;
-          const int byte = (wave * SO::FG + fl) * SO::FB + lg * SO::PS;
+          // (one pass in the kernels with half tiles: fragment wave nf + f at
+          // its column position; past the half tile's fragments nothing is
+          // staged and the stores below skip those columns, all past N)
+          if (HALF && f >= nf) continue;
+          const int byte = (HALF ? (wave * nf + f) * SO::FB : (wave * SO::FG + fl) * SO::FB) + lg * SO::PS;
           char* dst = ob + row * SO::PRB + (((byte >> 4) ^ (row & SO::SWM)) << 4) + (byte & 15);
           if constexpr (SO::F32OUT) *reinterpret_cast<f4_t*>(dst) = acc[f][tj];
           else if constexpr (EPI == Epi::SWIGLU_F16) *reinterpret_cast<uint32_t*>(dst) = ow[f][tj].x;
@@ -773,9 +803,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
   for (int f = 0; f < WF; ++f) {
     const int n = ncol[f];
-    if (n >= p.N) continue;
+    if (f >= nf || n >= p.N) continue;
     // a fragment of 16 columns lies wholly below or above rope_cols (a multiple of 64)
-    const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * WF + f) * 16 < p.rope_cols;
+    const bool rope = EPI == Epi::ROPE_F16 && n0 + (wave * nf + f) * 16 < p.rope_cols;
     const int pidx = (n & 63) >> 1;  // this lane's first (cos, sin) pair of the head
 #pragma unroll
     for (int tj = 0; tj < TJ; ++tj) {
