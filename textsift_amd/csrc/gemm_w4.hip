@@ -211,32 +211,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
     soff[f] = (uint32_t)(n * nb + lg) * 4u;
   }
 
-  // ---- activation rows this lane copies (rows past the tile read the
-  // tile's last row; their outputs are never stored)
-  const uint16_t* __restrict__ xsrc[XS];
-  xsrc[0] = static_cast<const uint16_t*>(p.x);
-  if constexpr (XS == 2) xsrc[1] = p.x_lo;
-  int xoff[XI];
-#pragma unroll
-  for (int m = 0; m < XI; ++m) {
-    const int r = (m * NW + wave) * 4 + lg;
-    const int lr = row0 + min(r, rows - 1);
-    const int g = p.row_map ? p.row_map[lr] : lr;
-    xoff[m] = g * p.ldx + ((l16 ^ (r & 15)) << 3);
-  }
-
-  // (byte offsets as unsigned 32-bit values from a uniform base: the loads
-  // take the scalar-base + 32-bit-offset form, no 64-bit address arithmetic)
-  auto load_x = [&](int c, int buf) {
-#pragma unroll
-    for (int pl = 0; pl < XS; ++pl)
-#pragma unroll
-      for (int m = 0; m < XI; ++m) {
-        _Float16* dst = xs_lds + (buf * XS + pl) * PLANE + (m * NW + wave) * 512;
-        copy16_to_lds(reinterpret_cast<const char*>(xsrc[pl]) + (uint32_t)(xoff[m] + c * KC) * 2u, (lds_ptr_t)dst);
-      }
-  };
-
+  // ---- chunk 0's weights and the bias are issued here: their addresses
+  // need only the tile entry, so their latency overlaps the reads of the
+  // activation rows' indices (row_map) below.
   using WR = std::conditional_t<W16, W16Reg, u4_t>;
   WR wraw[WF], wnext[WF];
   uint32_t sz[WF], sznext[WF];
@@ -266,25 +243,27 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   int ncol[WF];
 #pragma unroll
   for (int f = 0; f < WF; ++f) ncol[f] = n0 + (wave * nf + f) * 16 + 4 * lg;
-  f4_t acc[WF][TJ];
-  {
-    u2_t braw[WF];
+  u2_t braw[WF];
 #pragma unroll
-    for (int f = 0; f < WF; ++f) braw[f] = u2_t{0u, 0u};
-    if (BIAS) {
-      if ((p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(BIAS) & 7) == 0) {
+  for (int f = 0; f < WF; ++f) braw[f] = u2_t{0u, 0u};
+  if (BIAS) {
+    if ((p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(BIAS) & 7) == 0) {
 #pragma unroll
-        for (int f = 0; f < WF; ++f) braw[f] = *reinterpret_cast<const u2_t*>(BIAS + min(ncol[f], p.N - 4));
-      } else {
+      for (int f = 0; f < WF; ++f) braw[f] = *reinterpret_cast<const u2_t*>(BIAS + min(ncol[f], p.N - 4));
+    } else {
 #pragma unroll
-        for (int f = 0; f < WF; ++f) {
-          uint32_t h[4];
+      for (int f = 0; f < WF; ++f) {
+        uint32_t h[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) h[r] = BIAS[min(ncol[f] + r, p.N - 1)];
-          braw[f] = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-        }
+        for (int r = 0; r < 4; ++r) h[r] = BIAS[min(ncol[f] + r, p.N - 1)];
+        braw[f] = u2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
     }
+  }
+  // (called once the first chunk's loads are issued: waiting for the bias
+  // then overlaps their latency instead of preceding them)
+  f4_t acc[WF][TJ];
+  auto init_acc = [&]() {
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
       const uint32_t bw[2] = {braw[f].x, braw[f].y};
@@ -296,7 +275,39 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
     }
+  };
+  // (not in the kernels with half tiles: the two register sets then held
+  // across the row indices' reads spill)
+  if constexpr (CT == 0 && !HALF)
+    if (!idle) load_w(std::integral_constant<int, WF>{}, 0, wraw, sz);
+
+  // ---- activation rows this lane copies (rows past the tile read the
+  // tile's last row; their outputs are never stored)
+  const uint16_t* __restrict__ xsrc[XS];
+  xsrc[0] = static_cast<const uint16_t*>(p.x);
+  if constexpr (XS == 2) xsrc[1] = p.x_lo;
+  int xoff[XI];
+#pragma unroll
+  for (int m = 0; m < XI; ++m) {
+    const int r = (m * NW + wave) * 4 + lg;
+    const int lr = row0 + min(r, rows - 1);
+    const int g = p.row_map ? p.row_map[lr] : lr;
+    xoff[m] = g * p.ldx + ((l16 ^ (r & 15)) << 3);
   }
+
+  // (byte offsets as unsigned 32-bit values from a uniform base: the loads
+  // take the scalar-base + 32-bit-offset form, no 64-bit address arithmetic)
+  auto load_x = [&](int c, int buf) {
+#pragma unroll
+    for (int pl = 0; pl < XS; ++pl)
+#pragma unroll
+      for (int m = 0; m < XI; ++m) {
+        _Float16* dst = xs_lds + (buf * XS + pl) * PLANE + (m * NW + wave) * 512;
+        copy16_to_lds(reinterpret_cast<const char*>(xsrc[pl]) + (uint32_t)(xoff[m] + c * KC) * 2u, (lds_ptr_t)dst);
+      }
+  };
+
+
 
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
   // (fragments 0 .. nfc - 1)
@@ -393,6 +404,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       for (int f = 0; f < CT; ++f)
         gam[f] = *reinterpret_cast<const u4_t*>(p.nrm_gamma + (5 * (q >> 1) + f) * 16 + 8 * (q & 1));
     }
+    init_acc();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (NORM) {
@@ -476,7 +488,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
         if constexpr (GROUPED) __builtin_amdgcn_s_setprio(0);
       };
       load_x(0, 0);
-      if (!idle) load_w(nfc, 0, wraw, sz);
+      if constexpr (HALF)
+        if (!idle) load_w(nfc, 0, wraw, sz);
+      init_acc();
       int c = 0;
       for (; c + 2 < C; c += 2) {
         step(c, 0, wraw, sz, wnext, sznext);
@@ -1164,20 +1178,12 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   int ncol[WF];
 #pragma unroll
   for (int f = 0; f < WF; ++f) ncol[f] = (wave * WF + f) * 16 + 4 * lg;
+  // the bias is loaded before the first chunks and widened after they are
+  // issued, so that its latency overlaps theirs
+  u2_t braw[WF];
+#pragma unroll
+  for (int f = 0; f < WF; ++f) braw[f] = p.bias ? *reinterpret_cast<const u2_t*>(p.bias + ncol[f]) : u2_t{0u, 0u};
   f4_t acc[WF][TJ];
-#pragma unroll
-  for (int f = 0; f < WF; ++f) {
-    // the bias widens as k_gemm_w4 widens it (the two O forms agree bit for bit)
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias) {
-      const u2_t bw = *reinterpret_cast<const u2_t*>(p.bias + ncol[f]);
-      const uint32_t bwv[2] = {bw.x, bw.y};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bv[r] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bwv[r >> 1] >> (16 * (r & 1))));
-    }
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
-  }
 
   auto compute = [&](int c) {
     h2_t off[WF], offh[WF], sc[WF];
@@ -1208,6 +1214,16 @@ __global__ __launch_bounds__(64 * RN_NW, 1) void k_gemm_w4_rownorm(GemmArgs p, c
   for (int i = 0; i < PD && i < C; ++i) {
     load_w(i);
     load_x(i, i);
+  }
+#pragma unroll
+  for (int f = 0; f < WF; ++f) {
+    // the bias widens as k_gemm_w4 widens it (the two O forms agree bit for bit)
+    const uint32_t bwv[2] = {braw[f].x, braw[f].y};
+    float bv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[r] = (float)__builtin_bit_cast(_Float16, (uint16_t)(bwv[r >> 1] >> (16 * (r & 1))));
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[f][j] = f4_t{bv[0], bv[1], bv[2], bv[3]};
   }
 #pragma unroll
   for (int c = 0; c < C; ++c) {
