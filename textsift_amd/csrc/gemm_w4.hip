@@ -260,8 +260,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       }
     }
   }
-  // (called once the first chunk's loads are issued: waiting for the bias
-  // then overlaps their latency instead of preceding them)
+  // (the K-looped tiles call it once the first chunk's loads are issued:
+  // waiting for the bias then overlaps their latency instead of preceding them)
   f4_t acc[WF][TJ];
   auto init_acc = [&]() {
 #pragma unroll
@@ -385,6 +385,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
   [[maybe_unused]] WR wall[CT > 0 ? CT : 1][WF];
   [[maybe_unused]] uint32_t szall[CT > 0 ? CT : 1][WF];
   if constexpr (CT > 0) {
+    // (the all-K tiles widen the bias before their loads: after them it
+    // costs a spilled register and gains nothing at their sizes)
+    init_acc();
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
       load_x(c, c);
@@ -404,7 +407,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       for (int f = 0; f < CT; ++f)
         gam[f] = *reinterpret_cast<const u4_t*>(p.nrm_gamma + (5 * (q >> 1) + f) * 16 + 8 * (q & 1));
     }
-    init_acc();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if constexpr (NORM) {
