@@ -370,17 +370,31 @@ constexpr int BWS = RBLK / 32 + 1;  // bitmap words per expert in LDS (padded: r
 // the block routes to expert e. OR is order-independent, so the bitmap (and
 // everything derived from it) is deterministic. Entries with an expert id
 // outside [0, E) are ignored.
-__device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx, uint32_t* bits, int t0, int nt,
-                                                 int K, int E) {
+// This thread's token's K expert ids (token t0 + threadIdx.x; -1 past the
+// block's nt tokens and past K), loaded once and kept in registers.
+__device__ __forceinline__ void moe_load_ids(const int32_t* __restrict__ idx, int t0, int nt, int K, int (&ids)[MAXK]) {
+  const int tl = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) ids[k] = (k < K && tl < nt) ? idx[(size_t)(t0 + tl) * K + k] : -1;
+}
+
+__device__ __forceinline__ void moe_block_bitmap_ids(const int (&ids)[MAXK], uint32_t* bits, int E) {
   for (int i = threadIdx.x; i < E * BWS; i += blockDim.x) bits[i] = 0u;
   __syncthreads();
   const int tl = threadIdx.x;
-  if (tl < nt)
-    for (int k = 0; k < K; ++k) {
-      const int e = idx[(size_t)(t0 + tl) * K + k];
-      if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * BWS + (tl >> 5)], 1u << (tl & 31));
-    }
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int e = ids[k];
+    if ((unsigned)e < (unsigned)E) atomicOr(&bits[e * BWS + (tl >> 5)], 1u << (tl & 31));
+  }
   __syncthreads();
+}
+
+__device__ __forceinline__ void moe_block_bitmap(const int32_t* __restrict__ idx, uint32_t* bits, int t0, int nt,
+                                                 int K, int E) {
+  int ids[MAXK];
+  moe_load_ids(idx, t0, nt, K, ids);
+  moe_block_bitmap_ids(ids, bits, E);
 }
 
 // pre[e][w] = tokens of the block routed to e among words 0 .. w-1 of the
@@ -602,7 +616,9 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
                                                           int tile_t) {
   __shared__ uint32_t bits[256 * BWS];
   __shared__ int32_t off[256], toff[256], wsum[2][RBLK / 64];
-  moe_block_bitmap(idx, bits, 0, T, K, E);
+  int ids[MAXK];  // this thread's token's expert ids, read once
+  moe_load_ids(idx, 0, T, K, ids);
+  moe_block_bitmap_ids(ids, bits, E);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   // rows c and tiles n of expert e = tid; inclusive scans within the wave
   int c = 0;
@@ -650,10 +666,11 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_small(const int32_t* __restr
   if (tid >= T) return;
   const int wl = tid >> 5;
   const uint32_t below = (1u << (tid & 31)) - 1u;
-  for (int k = 0; k < K; ++k) {
-    const size_t i = (size_t)tid * K + k;
-    const int e = idx[i];
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int e = ids[k];
     if ((unsigned)e >= (unsigned)E) continue;
+    const size_t i = (size_t)tid * K + k;
     const int rank = pre[e * BWS + wl] + __popc(bits[e * BWS + wl] & below);
     const int pos = off[e] + rank;
     slot_token[pos] = tid;
@@ -682,6 +699,10 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_counts(const int32_t* __rest
   __shared__ uint16_t pre[256 * BWS];
   const int blk = blockIdx.x, t0 = blk * RBLK, ntok = min(RBLK, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  // this thread's token's expert ids, issued before the count loads so both
+  // latencies overlap, and kept for the slot assignment
+  int ids[MAXK];
+  moe_load_ids(idx, t0, ntok, K, ids);
   // Per-expert sums over the tiles, in G parts of the tile range. With E a
   // multiple of 4 a thread loads 16 bytes (4 experts' counts) per tile:
   // E2 / 4 expert groups x G = 4 RBLK / E2 parts; otherwise one expert per
@@ -737,7 +758,7 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_counts(const int32_t* __rest
       psum[1][q * E2 + e0] = sb[0];
     }
   }
-  moe_block_bitmap(idx, bits, t0, ntok, K, E);  // (its barriers also publish psum)
+  moe_block_bitmap_ids(ids, bits, E);  // (its barriers also publish psum)
   // rows c and tiles n of expert e = tid; inclusive scans within the wave
   int c = 0, below = 0;
   if (tid < E) {
@@ -786,10 +807,11 @@ __global__ __launch_bounds__(RBLK) void k_moe_route_counts(const int32_t* __rest
   if (tid >= ntok) return;
   const int wl = tid >> 5;
   const uint32_t lower = (1u << (tid & 31)) - 1u;
-  for (int k = 0; k < K; ++k) {
-    const size_t i = (size_t)(t0 + tid) * K + k;
-    const int e = idx[i];
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int e = ids[k];
     if ((unsigned)e >= (unsigned)E) continue;
+    const size_t i = (size_t)(t0 + tid) * K + k;
     const int rank = pre[e * BWS + wl] + __popc(bits[e * BWS + wl] & lower);
     const int pos = off[e] + rank;
     slot_token[pos] = t0 + tid;
