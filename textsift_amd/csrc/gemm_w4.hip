@@ -307,8 +307,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void k_gemm_w4(GemmArgs p) {
       }
   };
 
-
-
   // one 128-wide K chunk of MFMAs from LDS buffer buf and the weights in wraw / sz
   // (fragments 0 .. nfc - 1)
   auto compute = [&](auto nfc, int buf, const WR (&wr)[WF], const uint32_t (&szc)[WF]) {
