@@ -68,10 +68,10 @@ void* pfhip_buffer_device_ptr(const pfhip_buffer* buf);
  * push: the kernel's uniform block (the reference's `Dims` struct bytes);
  * grid: accepted for interface parity and ignored — each HIP kernel derives
  * its launch geometry from `push` (workgroups here are not 64-thread WGSL
- * workgroups). Kernel names and push layouts are listed by
- * pfhip_kernel_names() and documented in INTEGRATION.md; the reference's 15
- * names (vulkan_backend.zig:51-112) keep their binding order and Dims
- * layout so its conformance fixtures run unchanged.
+ * workgroups). pfhip_kernel_names() lists every registered kernel as one
+ * "name bindings push_bytes" line; the reference's 15 names
+ * (vulkan_backend.zig:51-112) keep their binding order and Dims layout so
+ * its conformance fixtures run unchanged.
  *
  * An encoder records dispatches on the backend's stream; submit waits for
  * them, copies `n` bytes of `out` at `offset` into `dst` and releases the
