@@ -4,6 +4,8 @@ smaller tests would not reach: the router GEMM's top-4 epilogue on its
 weights) on each of their three tiles, the reference fixtures of the
 qmoe_gate_up / qmoe_down_scatter / zero_f32 kernels, and the forward's
 row-limit check. All calls go through the C ABI by kernel name."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -79,16 +81,19 @@ def test_router_topk_epilogue_bit_exact(be, kind, tile, T):
 
 # ---------------------------------------------------------------- MoE layer in the fp16 numerics
 
-@pytest.mark.parametrize("T,E,tile", [(2048, 128, 64),
-                                      (8192, 128, 128),   # the 16 x 2048 forward's tile
-                                      (37, 16, 16)])      # the all-K 16-token tile
-def test_moe_layer_fp16_vs_oracle(be, T, E, tile):
+@pytest.mark.parametrize("T,E,tile,dim", [(2048, 128, 64, 640),
+                                          (8192, 128, 128, 640),   # the 16 x 2048 forward's tile
+                                          (8192, 128, 128, 384),   # down's N = 256 + 128: the half column tile
+                                          (37, 16, 16, 640)])      # the all-K 16-token tile
+def test_moe_layer_fp16_vs_oracle(be, T, E, tile, dim):
     """moe_ffn in the forward's fp16 numerics: the gemm_w4 grouped SwiGLU
     and down kernels on scale-folded weights (the launches the forward makes),
     with the forward's tile choice, against the oracle's expert-major dispatch
     (browser/inference/expert.ts:104-212, zig/wasm_exports.zig:560-1055) on
-    the GPU's routing. Config 3: Zipf(1.1)-skewed router."""
-    cfg = PF_CONFIG
+    the GPU's routing. Config 3: Zipf(1.1)-skewed router. dim = 384 (hidden and
+    intermediate size) runs the down GEMM's last column tile, 128 of its 256
+    rows, as the half tile (two fragments on each of the four waves)."""
+    cfg = dataclasses.replace(PF_CONFIG, hidden_size=dim, intermediate_size=dim)
     D, F, K = cfg.hidden_size, cfg.intermediate_size, cfg.num_experts_per_tok
     x = synth.to_fp16_bits(synth.normal(710 + T, T * D)).reshape(T, D)
     rw_, rb = synth.zipf_router(711, D, E)
@@ -115,7 +120,7 @@ def test_moe_layer_fp16_vs_oracle(be, T, E, tile):
     ref = oracle.expert_dispatch(cfg, w, 0, oracle.fp16_to_f32(x), ridx, rwt * np.float32(0.25), n_slices=8)
     err = rel_err_norm(f16(y), f16(ref))
     same = float(np.mean(y == ref))
-    print(f"moe fp16 T={T} E={E} tile={tile}: rel-err {err:.3e}, identical {same:.4f}; "
+    print(f"moe fp16 T={T} E={E} tile={tile} dim={dim}: rel-err {err:.3e}, identical {same:.4f}; "
           f"load max {counts.max()} min {counts.min()} (experts used {int((counts > 0).sum())})")
     assert err < 2e-3
     # the folded fp16 weights and the fp16 SwiGLU output each add one fp16
