@@ -62,6 +62,7 @@ KERNEL_LABELS = [
     ("moe_count", ("k_moe_count",)),
     ("moe_scan", ("k_moe_scan",)),
     ("moe_scatter", ("k_moe_scatter",)),
+    ("embed_rms_norm", ("k_embed_rms_norm",)),
     ("embed_lookup_int4", ("k_embed",)),
     ("rms_norm", ("k_rms_norm",)),
     ("copy_lds", ("k_copy16_lds",)),

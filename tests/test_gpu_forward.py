@@ -6,6 +6,8 @@ Bars: logits within rel-err 2e-3 (normwise) and per-token argmax agreement
 the GPU's own input residual), which isolates one layer's error from the
 accumulation of the layers before it. Every test runs for both GEMM input
 precisions (fp16 with scale-folded weights, and the f32 hi/lo split)."""
+import struct
+
 import numpy as np
 import pytest
 
@@ -85,6 +87,40 @@ def test_forward_is_deterministic(small):
         be.forward(synth.token_ids(951 + t, t, V), np.ones(t, np.uint8))
     again = be.forward(ids, np.ones(T, np.uint8)).as_matrix()
     assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+
+
+def test_embedding_and_first_norm_taps(small):
+    """The forward's first step (fp16 numerics: the gather and the first
+    RMSNorm in one kernel) against the separate operations: the embedded rows
+    are oracle.embed_lookup's bits (out-of-range ids give zero rows) and the
+    normalised rows are the bits the stand-alone rms_norm kernel makes of
+    them; T = 37 leaves a partial group of 4 rows."""
+    w, be = small
+    T, D = 37, PF_CONFIG.hidden_size
+    ids = synth.token_ids(905, T, V)
+    ids[[0, 17, 36]] = [-3, V, V + 100]
+    m = be.model
+    m.enable_taps(True)
+    try:
+        be.forward(ids, np.ones(T, np.uint8))
+        emb = m.tap("embed", np.uint16, T * D).reshape(T, D)
+        xn0 = m.tap("xn0", np.uint16, T * D).reshape(T, D)
+    finally:
+        m.enable_taps(False)
+    assert np.array_equal(emb, oracle.embed_lookup(w["embed.int4"], w["embed.scales"], w["embed.zp"], ids, V, D))
+    assert not emb[[0, 17, 36]].any()
+    if be.precision != _native.PRECISION_FP16:
+        return
+    raw = m.backend
+    g = w["layers.0.input_layernorm"]
+    bx, bg, bo = raw.buffer(emb), raw.buffer(g), raw.buffer(nbytes=T * D * 2)
+    try:
+        raw.dispatch("rms_norm", [bx, bg, bo], struct.pack("<IIfI", T, D, PF_CONFIG.rms_norm_eps, 0))
+        ref = bo.read(np.uint16).reshape(T, D)
+    finally:
+        for b_ in (bx, bg, bo):
+            b_.release()
+    assert np.array_equal(xn0, ref)
 
 
 def test_per_layer_taps_vs_oracle_block(small):

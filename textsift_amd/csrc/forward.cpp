@@ -430,10 +430,16 @@ static void run_forward(pfhip_model* m, const int32_t* ids, const uint8_t* mask,
   // routing plan (no separate plan kernel: one launch fewer per layer)
   const bool plan_in_router = fused_topk && router_tile == 16 && M <= 16;
 
-  embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
-               M, (int)c.vocab, D);
-  if (f16) rms_norm_f16(b, s.h0, m->layers[0].ln_in, s.xn_hi, M, D, c.eps);
-  else rms_norm_split(b, s.h0, m->layers[0].ln_in, s.xn_hi, s.xn_lo, M, D, c.eps);
+  if (f16) {
+    embed_rms_norm_f16(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids,
+                       m->layers[0].ln_in, s.h0, s.xn_hi, M, (int)c.vocab, D, c.eps);
+  } else {
+    embed_lookup(b, W<uint8_t>(m, "embed.int4"), W<uint16_t>(m, "embed.scales"), W<uint8_t>(m, "embed.zp"), ids, s.h0,
+                 M, (int)c.vocab, D);
+    rms_norm_split(b, s.h0, m->layers[0].ln_in, s.xn_hi, s.xn_lo, M, D, c.eps);
+  }
+  record_tap(m, "embed", s.h0, (size_t)M * D * 2);
+  record_tap(m, "xn0", s.xn_hi, (size_t)M * D * 2);
   uint16_t* h = s.h0;
   uint16_t* hn = s.h1;
   for (size_t l = 0; l < m->layers.size(); ++l) {

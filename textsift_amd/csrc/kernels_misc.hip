@@ -179,6 +179,88 @@ __global__ __launch_bounds__(256) void k_rms_norm4(const uint16_t* __restrict__ 
   }
 }
 
+// The embedding gather and the model's first RMSNorm in one pass (fp16
+// numerics, D = 128 NU): embed_lookup_int4 (zig/wasm_exports.zig:1523-1573)
+// then rms_norm (:186-218). The units are k_rms_norm4's (a wave takes 4 rows,
+// lane l the 16-byte units u = 64 i + l, row u / (D / 8)), and a unit is
+// exactly what one k_embed thread makes of one dword of a table row: 8
+// nibbles -> fp16((q - zp) * scale). Each lane stores its embedded units (the
+// residual stream), widens them as k_rms_norm4 widens what it loads and
+// normalises them in k_rms_norm4's order, so both outputs are the bits of the
+// two-kernel form, without the embedded rows' write-then-read in between.
+// Ids outside [0, V) give a zero row (and a zero-row norm).
+template <int NU>
+__global__ __launch_bounds__(256) void k_embed_rms_norm4(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+                                                         const uint8_t* __restrict__ zp,
+                                                         const int32_t* __restrict__ ids,
+                                                         const uint16_t* __restrict__ g, uint16_t* __restrict__ h,
+                                                         uint16_t* __restrict__ out, int T, int V, float eps) {
+  constexpr int D = 128 * NU, UPR = D / 8, NB = D / 32, NZ = (NB + 1) / 2;
+  const int lane = threadIdx.x & 63;
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+  if (t0 >= T) return;
+  int id[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) id[r] = ids[min(t0 + r, T - 1)];
+  uint32_t w[NU];
+  uint16_t sb[NU];
+  uint8_t zb[NU];
+  int row[NU], dw[NU];
+  bool ok[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int u = 64 * i + lane;
+    row[i] = u / UPR;
+    dw[i] = u - row[i] * UPR;  // the dword of the table row (8 values)
+    const int idr = row[i] == 0 ? id[0] : row[i] == 1 ? id[1] : row[i] == 2 ? id[2] : id[3];
+    ok[i] = idr >= 0 && idr < V;
+    const uint32_t rr = ok[i] ? (uint32_t)idr : 0u;  // out-of-range ids read row 0, stored as 0
+    w[i] = reinterpret_cast<const uint32_t*>(q + (size_t)rr * (D / 2))[dw[i]];
+    sb[i] = s[(size_t)rr * NB + (dw[i] >> 2)];
+    zb[i] = zp[(size_t)rr * NZ + (dw[i] >> 3)];
+  }
+  float v[NU][8];
+  float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    u4_t res = {0u, 0u, 0u, 0u};
+    if (ok[i]) {
+      const float sc = wasm_h2f(sb[i]);
+      const int z = ((dw[i] >> 2) & 1) ? (zb[i] >> 4) : (zb[i] & 0xF);
+      float e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = (float)((int)((w[i] >> (4 * j)) & 0xFu) - z) * sc;
+      const u2_t a = to_f16x4_z(e), c = to_f16x4_z(e + 4);
+      res = u4_t{a.x, a.y, c.x, c.y};
+    }
+    const int t = t0 + row[i];
+    if (t < T) *reinterpret_cast<u4_t*>(h + (size_t)t * D + dw[i] * 8) = res;
+    h4_to_f(u2_t{res.x, res.y}, v[i]);
+    h4_to_f(u2_t{res.z, res.w}, v[i] + 4);
+    float sq = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) sq += v[i][r] * v[i][r];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ss[r] += row[i] == r ? sq : 0.0f;
+  }
+  float inv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) inv[r] = 1.0f / sqrtf(wave_sum(ss[r]) * (1.0f / (float)D) + eps);
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int t = t0 + row[i];
+    const float ir = row[i] == 0 ? inv[0] : row[i] == 1 ? inv[1] : row[i] == 2 ? inv[2] : inv[3];
+    const u4_t gw = *reinterpret_cast<const u4_t*>(g + dw[i] * 8);
+    float gm[8], y[8];
+    h4_to_f(u2_t{gw.x, gw.y}, gm);
+    h4_to_f(u2_t{gw.z, gw.w}, gm + 4);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = v[i][r] * ir * gm[r];
+    const u2_t lo = to_f16x4_z(y), hi = to_f16x4_z(y + 4);
+    if (t < T) *reinterpret_cast<u4_t*>(out + (size_t)t * D + dw[i] * 8) = u4_t{lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
 // add_rmsnorm_fp16_to_f32 (:288-350): sum = a + b (fp16 store), sumsq of the
 // unrounded f32 sum, normalise the rounded sum.
 template <int MODE>
@@ -1169,6 +1251,22 @@ void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const u
   else
     hipLaunchKernelGGL(k_embed<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, b->stream, q, s, zp, ids, out,
                        T, V, D);
+  PF_HIP(hipGetLastError());
+}
+
+void embed_rms_norm_f16(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
+                        const uint16_t* g, uint16_t* h, uint16_t* out, int T, int V, int D, float eps) {
+  const bool fused = D == 640 && ((reinterpret_cast<uintptr_t>(q) & 3) | ((reinterpret_cast<uintptr_t>(g) |
+                                   reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(out)) & 15)) == 0;
+  if (!fused) {
+    embed_lookup(b, q, s, zp, ids, h, T, V, D);
+    rms_norm_f16(b, h, g, out, T, D, eps);
+    return;
+  }
+  if (T <= 0) return;
+  ProfScope ps(b, "embed_rms_norm");
+  hipLaunchKernelGGL(k_embed_rms_norm4<5>, dim3((unsigned)((T + 15) / 16)), dim3(256), 0, b->stream, q, s, zp, ids, g,
+                     h, out, T, V, eps);
   PF_HIP(hipGetLastError());
 }
 

@@ -192,6 +192,11 @@ void w4_prepare(pfhip_backend* b, const uint8_t* w, const uint16_t* ws, const ui
 void embed_lookup(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
                   uint16_t* out, int T, int V, int D, bool stream_out = false);
 
+// embed_lookup into h, then rms_norm_f16 of h into out: one kernel for the
+// model's width (D = 640, aligned operands), bit-identical to the two.
+void embed_rms_norm_f16(pfhip_backend* b, const uint8_t* q, const uint16_t* s, const uint8_t* zp, const int32_t* ids,
+                        const uint16_t* g, uint16_t* h, uint16_t* out, int T, int V, int D, float eps);
+
 // RMSNorm family. The *_split variants write the f32 result as hi/lo fp16
 // planes (norm_hi, norm_lo) for SPLIT GEMM inputs.
 void rms_norm_f16(pfhip_backend* b, const uint16_t* x, const uint16_t* g, uint16_t* out, int T, int D, float eps);
